@@ -1,0 +1,210 @@
+/*
+ * smx.h - C ABI of the MI355X (gfx950) batch-1 Q4_0 decode path.
+ *
+ * Every entry point:
+ *   - takes the HIP stream as an opaque `void*` first (NULL = the default
+ *     stream), then raw device pointers and integer sizes;
+ *   - validates its arguments on the host before touching the GPU and
+ *     returns SMX_EINVAL (with a message from smx_last_error()) when they are
+ *     wrong, so a bad call never reaches a kernel;
+ *   - otherwise enqueues its kernels on `stream` and returns 0, or the
+ *     hipError_t value reported by the launch;
+ *   - never allocates, never synchronises, never throws across the ABI, and
+ *     is safe to record into a HIP graph.
+ *
+ * The reference's only native C ABI on this path is
+ *   extern "C" void launch_head_q6s(void* stream, uint8_t* x, uint8_t* w,
+ *                                   uint8_t* y, int rows, int decode)
+ * (src/spark_vllm_ascend/native/head/head_q6.asc:35, declared at
+ * src/spark_vllm_ascend/native/head/extension.cpp:6) plus the argument checks
+ * of its TORCH_CHECK wrapper (extension.cpp:8-10).  The rest of the
+ * reference's decode path is one DSL megakernel (kernels/layer.py:48-109);
+ * each function below replaces one of its stages and cites it.
+ *
+ * Tensor formats (all row-major, contiguous):
+ *   bf16   : uint16 bit patterns of bfloat16.
+ *   Q4_0   : GGUF ggml type 2.  A row of k weights is k/32 blocks of 18
+ *            bytes: fp16 little-endian scale d, then 16 bytes qs; element
+ *            j<16 is (qs[j] & 15) - 8, element j>=16 is (qs[j-16] >> 4) - 8,
+ *            value = d * element.
+ *   KV cache: [num_blocks, block_size, num_kv_heads, head_dim] bf16, one
+ *            tensor for K and one for V (vLLM's paged layout).
+ */
+#ifndef SMX_H
+#define SMX_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SMX_ABI_VERSION 1
+
+/* Return codes besides 0 and hipError_t values. */
+#define SMX_EINVAL 10001      /* an argument failed validation */
+#define SMX_EUNSUPPORTED 10002 /* a valid shape this build has no kernel for */
+
+/* ABI version of the loaded library (SMX_ABI_VERSION it was built with). */
+int smx_abi_version(void);
+
+/* Text of the last validation error raised on the calling thread. */
+const char* smx_last_error(void);
+
+/*
+ * Q4_0 -> bf16 dequantisation, bit-exact: out[r, j] = RNE_bf16(float(d) * q).
+ * w: n rows of k/32 Q4_0 blocks; out: [n, k] bf16.  Requires k % 32 == 0.
+ * Replaces unpack_q4 + gguf dequantize + .bfloat16()
+ * (src/spark_vllm_ascend/integration/weights.py:28-40,
+ *  src/tools/deployment/prepare_model.py:62-64).
+ */
+int smx_q4_0_dequant_bf16(void* stream, const void* w, void* out,
+                          int64_t n, int64_t k);
+
+/*
+ * Q4_0 dequant-fused GEMV for one activation row:
+ *   y[r] = RNE_bf16( sum_b float(d_rb) * sum_j x[32b+j] * q_rbj )
+ * with fp32 accumulation.  x: [k] bf16; w: [n, k/32] Q4_0 blocks;
+ * y: [n] bf16.  Requires k % 32 == 0 and n >= 1.
+ * Replaces GemvStage.calculate and its callers (NativeLinear.execute_o,
+ * execute_down, NativeUp, FusedQkvStage: src/spark_vllm_ascend/kernels/
+ * linear.py:16-200,339-370, kernels/qkv.py:201-236).
+ */
+int smx_q4_0_gemv(void* stream, const void* x, const void* w, void* y,
+                  int64_t n, int64_t k);
+
+/*
+ * Fused gate/up Q4_0 GEMV + SwiGLU for one activation row.
+ * w: [2*d, k] Q4_0 holding the gate rows [0, d) then the up rows [d, 2d)
+ * (vLLM MergedColumnParallelLinear order).  out[i] =
+ *   RNE_bf16( silu(g_i) * u_i ), g_i = RNE_bf16(gate GEMV), u_i likewise.
+ * Replaces NativeUp.execute + activate_native
+ * (src/spark_vllm_ascend/kernels/linear.py:540-611), with SwiGLU in place of
+ * the reference model's GELU.
+ */
+int smx_q4_0_gemv_swiglu(void* stream, const void* x, const void* w,
+                         void* out, int64_t d, int64_t k);
+
+/*
+ * Split-KV flash-decode attention, one partial per (sequence, split, q head).
+ *   q: [num_seqs, n_q, head_dim] bf16
+ *   k_cache, v_cache: [num_blocks, block_size, n_kv, head_dim] bf16
+ *   block_table: [num_seqs, max_blocks] int32, seq_lens: [num_seqs] int32
+ *   partial_o: [num_seqs, num_splits, n_q, head_dim] fp32 (normalised)
+ *   partial_lse: [num_seqs, num_splits, n_q] fp32 (natural log; -inf for an
+ *     empty split)
+ * Split s of a sequence of length L covers tokens
+ *   [s*T, min(L, (s+1)*T)), T = 32 * ceil(ceil(L / num_splits) / 32),
+ * where L = min(seq_lens[r], max_blocks * block_size).
+ * Scores are q.k * scale in fp32; probabilities are rounded to bf16 before
+ * they multiply V, and the running sum uses the unrounded fp32 values.
+ * A block-table entry outside [0, num_blocks) is never dereferenced; the
+ * partials of that split become NaN.
+ * Supports head_dim == 128, n_q == 4 * n_kv (GQA 4:1) and power-of-two
+ * block_size in [32, 4096].
+ * Replaces AttentionStage (src/spark_vllm_ascend/kernels/attention.py:18-293).
+ */
+int smx_splitkv_decode(void* stream, const void* q, const void* k_cache,
+                       const void* v_cache, const int32_t* block_table,
+                       const int32_t* seq_lens, float* partial_o,
+                       float* partial_lse, int32_t num_seqs,
+                       int32_t num_splits, int32_t max_blocks,
+                       int32_t num_blocks, int32_t block_size, int32_t n_q,
+                       int32_t n_kv, int32_t head_dim, float scale);
+
+/*
+ * Log-sum-exp merge of the split partials:
+ *   w_s = exp(lse_s - max_s lse) / sum, out = RNE_bf16(sum_s w_s * o_s).
+ * out: [num_seqs, n_q, head_dim] bf16.
+ * Replaces merge_attention (src/spark_vllm_ascend/kernels/vector.py:45-83)
+ * without the reference model's sigmoid output gate.
+ */
+int smx_lse_merge(void* stream, const float* partial_o,
+                  const float* partial_lse, void* out, int32_t num_seqs,
+                  int32_t num_splits, int32_t n_q, int32_t head_dim);
+
+/*
+ * Residual add + RMSNorm over rows of `hidden` values:
+ *   s = float(x) + float(residual)            (residual may be NULL: s = x)
+ *   residual_out = RNE_bf16(s)
+ *   y = RNE_bf16( s * (1 / sqrt(sum(s^2)/hidden + eps)) * float(gamma) )
+ * residual_out may alias residual; a NULL residual_out is not written.
+ * All bf16 tensors 16-byte aligned; hidden % 8 == 0 and hidden <= 16384.
+ * Replaces norm_ub / NativePool.final_norm
+ * (src/spark_vllm_ascend/kernels/linear.py:202-224,299-305).
+ */
+int smx_add_rmsnorm(void* stream, const void* x, const void* residual,
+                    const void* gamma, void* y, void* residual_out,
+                    int64_t rows, int64_t hidden, float eps);
+
+/*
+ * Per-head q/k RMSNorm + neox RoPE + paged KV write, for num_tokens tokens.
+ *   qkv: [num_tokens, (n_q + 2*n_kv) * head_dim] bf16 (q heads, k heads,
+ *        v heads), the fused QKV GEMV output.
+ *   q_gamma, k_gamma: [head_dim] bf16; eps for both norms.
+ *   cos_sin: [max_position, head_dim] bf16, row p = cos(p*f_i) for
+ *        i < head_dim/2 then sin(p*f_i) (vLLM cos_sin_cache layout).
+ *   positions: [num_tokens] int64; slot_mapping: [num_tokens] int64
+ *        (-1 = do not write this token's K/V).
+ *   q_out: [num_tokens, n_q, head_dim] bf16.
+ * Each norm output and each rotated value is rounded to bf16.
+ * Replaces FusedQkvStage.calculate_rotated/store8 RoPE + cache write
+ * (src/spark_vllm_ascend/kernels/qkv.py:179-236); the q/k norm has no
+ * counterpart in the reference model.
+ */
+int smx_qknorm_rope_kv_write(void* stream, const void* qkv,
+                             const void* q_gamma, const void* k_gamma,
+                             const void* cos_sin, const int64_t* positions,
+                             const int64_t* slot_mapping, void* q_out,
+                             void* k_cache, void* v_cache, int32_t num_tokens,
+                             int32_t n_q, int32_t n_kv, int32_t head_dim,
+                             int32_t num_blocks, int32_t block_size,
+                             int32_t max_position, float eps);
+
+/*
+ * SwiGLU on a [rows, 2*d] bf16 gate|up tensor: out[r, i] =
+ * RNE_bf16(silu(g) * u), g = gate_up[r, i], u = gate_up[r, d + i].
+ */
+int smx_silu_mul(void* stream, const void* gate_up, void* out, int64_t rows,
+                 int64_t d);
+
+/*
+ * Embedding row gather: out[t, :] = table[ids[t], :] (bf16); an id outside
+ * [0, vocab) writes a zero row.
+ * Replaces VocabParallelEmbedding's lookup
+ * (src/spark_vllm_ascend/plugin/spark2_5.py:320-325,362).
+ */
+int smx_embedding(void* stream, const void* table, const int64_t* ids,
+                  void* out, int64_t num_tokens, int64_t vocab,
+                  int64_t hidden);
+
+/*
+ * Greedy token: out_ids[r] = argmax_j logits[r, j] (bf16), lowest index on
+ * ties, NaN counts as the largest value.  Replaces vLLM's greedy sampler at
+ * temperature 0 (src/tools/benchmark/data/request.json:5).
+ */
+int smx_argmax_bf16(void* stream, const void* logits, int64_t rows,
+                    int64_t vocab, int64_t* out_ids);
+
+/*
+ * Advance a decode batch by one token, on the device, so that one captured
+ * graph serves every step:
+ *   ids[r] = next_ids[r]; positions[r] += 1; seq_lens[r] = positions[r] + 1;
+ *   slot_mapping[r] = block_table[r, p / block_size] * block_size
+ *                     + p % block_size  (p = new position; -1 when the
+ *                     table has no entry for p);
+ *   tokens_out[r, p] = next_ids[r] when tokens_out != NULL and p < max_len.
+ * The slot formula is the reference's slot mapping
+ * (src/spark_vllm_ascend/integration/slot_mapping.py:8-33).
+ */
+int smx_decode_advance(void* stream, const int64_t* next_ids, int64_t* ids,
+                       int64_t* positions, int32_t* seq_lens,
+                       int64_t* slot_mapping, const int32_t* block_table,
+                       int64_t* tokens_out, int32_t rows, int32_t max_blocks,
+                       int32_t block_size, int32_t max_len);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SMX_H */

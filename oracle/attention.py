@@ -1,0 +1,104 @@
+"""Paged GQA decode attention for the oracle -- test infrastructure.
+
+attention_f64     textbook softmax(q K^T * scale) V in float64 over the
+                  gathered, unpaged KV.  The reference for everything else.
+splitkv_partials  the reference's split-KV online softmax, AttentionStage
+                  (src/spark_vllm_ascend/kernels/attention.py:59-117): per
+                  tile, m' = max(m, tile max); alpha = exp(m - m'); p =
+                  exp(s - m') in fp32; sum = sum * alpha + sum(p); acc = acc *
+                  alpha + bf16(p) V; partial = acc / sum, lse = log(sum) + m.
+lse_merge         merge_attention (src/spark_vllm_ascend/kernels/vector.py:
+                  45-83) without the output gate: w_s = exp(lse_s - max) /
+                  sum, out = bf16(sum_s w_s o_s).
+
+Pins (tests/test_oracle_attention.py): split results merged equal the
+unsplit fp64 result for every split count; one split equals the unsplit
+result; ctx = 1 gives v_0; equal keys give the mean of V; permuting pages
+through the block table leaves the result unchanged; a partially filled last
+page masks its tail.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from .bf16 import round_bf16
+
+
+def gather_paged(cache: np.ndarray, table: np.ndarray, length: int) -> np.ndarray:
+    """cache [num_blocks, bs, n_kv, hd] -> [length, n_kv, hd] in token order."""
+    bs = cache.shape[1]
+    nblk = (length + bs - 1) // bs
+    pages = cache[np.asarray(table[:nblk], dtype=np.int64)]
+    return pages.reshape(nblk * bs, *cache.shape[2:])[:length]
+
+
+def attention_f64(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float) -> np.ndarray:
+    """q [n_q, hd]; k, v [L, n_kv, hd] -> out [n_q, hd] (float64)."""
+    n_q = q.shape[0]
+    n_kv = k.shape[1]
+    g = n_q // n_kv
+    out = np.empty((n_q, q.shape[1]), dtype=np.float64)
+    for h in range(n_q):
+        kh = k[:, h // g, :].astype(np.float64)
+        vh = v[:, h // g, :].astype(np.float64)
+        s = kh @ q[h].astype(np.float64) * scale
+        p = np.exp(s - s.max())
+        out[h] = p @ vh / p.sum()
+    return out
+
+
+def split_bounds(length: int, num_splits: int, align: int = 32):
+    """Token range of each split: T = align * ceil(ceil(L / S) / align)."""
+    per = -(-length // num_splits)
+    t = -(-per // align) * align
+    return [(s * t, min(length, (s + 1) * t)) for s in range(num_splits)]
+
+
+def splitkv_partials(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float,
+                     bounds, tile: int = 128):
+    """Per split: (partial_o [S, n_q, hd] fp32, lse [S, n_q] fp32), -inf lse
+    and zero output for an empty split."""
+    n_q, hd = q.shape
+    n_kv = k.shape[1]
+    g = n_q // n_kv
+    ns = len(bounds)
+    po = np.zeros((ns, n_q, hd), dtype=np.float32)
+    pl = np.full((ns, n_q), -np.inf, dtype=np.float32)
+    qf = q.astype(np.float32)
+    for si, (a, b) in enumerate(bounds):
+        if a >= b:
+            continue
+        for h in range(n_q):
+            kh = k[a:b, h // g, :].astype(np.float32)
+            vh = v[a:b, h // g, :].astype(np.float32)
+            m = np.float32(-np.inf)
+            ssum = np.float32(0.0)
+            acc = np.zeros(hd, dtype=np.float32)
+            for t0 in range(0, b - a, tile):
+                s = (kh[t0:t0 + tile] @ qf[h]).astype(np.float32) * np.float32(scale)
+                mn = np.float32(max(m, s.max()))
+                alpha = np.float32(np.exp(m - mn)) if np.isfinite(m) else np.float32(0.0)
+                p = np.exp((s - mn).astype(np.float32)).astype(np.float32)
+                ssum = np.float32(ssum * alpha + p.sum(dtype=np.float32))
+                acc = (acc * alpha + round_bf16(p) @ vh[t0:t0 + tile]).astype(np.float32)
+                m = mn
+            po[si, h] = acc / ssum
+            pl[si, h] = np.float32(np.log(ssum)) + m
+    return po, pl
+
+
+def lse_merge(po: np.ndarray, pl: np.ndarray) -> np.ndarray:
+    """(partial_o [S, n_q, hd], lse [S, n_q]) -> bf16-rounded float32 [n_q, hd]."""
+    mx = pl.max(axis=0)
+    z = np.where(np.isfinite(pl), np.exp((pl - mx).astype(np.float32)), 0.0).astype(np.float32)
+    w = (z / z.sum(axis=0)).astype(np.float32)
+    acc = np.einsum("sh,shd->hd", w, po).astype(np.float32)
+    return round_bf16(acc)
+
+
+def splitkv_decode(q, k_cache, v_cache, table, length, num_splits, scale, tile=128):
+    """Paged convenience wrapper: gather, split, merge."""
+    k = gather_paged(k_cache, table, length)
+    v = gather_paged(v_cache, table, length)
+    po, pl = splitkv_partials(q, k, v, scale, split_bounds(length, num_splits), tile)
+    return lse_merge(po, pl), po, pl

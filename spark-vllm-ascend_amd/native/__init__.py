@@ -1,0 +1,93 @@
+"""ctypes binding of libsmx.so, the C ABI declared in include/smx.h.
+
+The library is loaded after torch, so it binds to the HIP runtime torch
+already mapped (both carry the soname libamdhip64.so.7): device pointers and
+stream handles from torch are then valid in the library.  Nothing here falls
+back to another implementation: if the library is missing, every op raises.
+
+Wrappers validate devices, dtypes, contiguity and sizes the way the
+reference's TORCH_CHECK wrapper does (src/spark_vllm_ascend/native/head/
+extension.cpp:8-10), enqueue on the current stream and raise RuntimeError on
+a non-zero return code.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libsmx.so"
+ABI_VERSION = 1
+SMX_EINVAL = 10001
+SMX_EUNSUPPORTED = 10002
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I32 = ctypes.c_int32
+_F32 = ctypes.c_float
+
+# name -> argument types (all return int)
+SIGNATURES = {
+    "smx_abi_version": [],
+    "smx_q4_0_dequant_bf16": [_P, _P, _P, _I64, _I64],
+    "smx_q4_0_gemv": [_P, _P, _P, _P, _I64, _I64],
+    "smx_q4_0_gemv_swiglu": [_P, _P, _P, _P, _I64, _I64],
+    "smx_splitkv_decode": [_P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32,
+                           _I32, _I32, _F32],
+    "smx_lse_merge": [_P, _P, _P, _P, _I32, _I32, _I32, _I32],
+    "smx_add_rmsnorm": [_P, _P, _P, _P, _P, _P, _I64, _I64, _F32],
+    "smx_qknorm_rope_kv_write": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32,
+                                 _I32, _I32, _I32, _F32],
+    "smx_silu_mul": [_P, _P, _P, _I64, _I64],
+    "smx_embedding": [_P, _P, _P, _P, _I64, _I64, _I64],
+    "smx_argmax_bf16": [_P, _P, _I64, _I64, _P],
+    "smx_decode_advance": [_P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32],
+}
+
+_lib = None
+
+
+class SmxError(RuntimeError):
+    """A C-ABI call returned a non-zero code."""
+
+    def __init__(self, func: str, code: int, detail: str):
+        self.code = code
+        super().__init__(f"{func} failed with code {code}: {detail}")
+
+
+def load() -> ctypes.CDLL:
+    """Load libsmx.so once (after torch) and declare its signatures."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    try:  # bind to the HIP runtime torch uses when torch is present
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+    if not LIB_PATH.exists():
+        raise RuntimeError(
+            f"{LIB_PATH} is not built; run __graft_entry__.build() or "
+            "python spark-vllm-ascend_amd/native/build.py")
+    lib = ctypes.CDLL(str(LIB_PATH))
+    for name, argtypes in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        fn.restype = ctypes.c_int
+    lib.smx_last_error.argtypes = []
+    lib.smx_last_error.restype = ctypes.c_char_p
+    version = lib.smx_abi_version()
+    if version != ABI_VERSION:
+        raise RuntimeError(f"libsmx.so ABI {version} != expected {ABI_VERSION}")
+    _lib = lib
+    return lib
+
+
+def call(name: str, *args) -> None:
+    """Invoke a C-ABI function and raise SmxError on a non-zero return."""
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc != 0:
+        if rc in (SMX_EINVAL, SMX_EUNSUPPORTED):
+            detail = lib.smx_last_error().decode()
+        else:
+            detail = f"HIP error {rc}"
+        raise SmxError(name, rc, detail)

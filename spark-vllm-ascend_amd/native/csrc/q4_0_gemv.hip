@@ -1,0 +1,416 @@
+// Q4_0 (GGUF type 2) dequantisation and dequant-fused GEMV for gfx950.
+//
+// A Q4_0 row of k weights is k/32 blocks of 18 bytes: an fp16 scale d and 16
+// bytes qs holding element j (j < 16) in the low nibble of qs[j] and element
+// 16 + j in its high nibble; value = d * (nibble - 8).  This is the block
+// decode of src/spark_vllm_ascend/integration/weights.py:34-40.
+//
+// GEMV design (M = 1 is HBM-bound: 18 bytes per 32 weights, ~3.5 flop/B):
+//  * The weights are streamed in their GGUF layout.  A lane owns a block
+//    PAIR (36 bytes, 4-byte aligned) and fetches it with two 128-bit loads
+//    and one 32-bit load; 8 lanes cover 8 consecutive pairs of one row, so a
+//    wave reads 8 rows x 288 contiguous bytes per step.  The waves of a
+//    workgroup split K, which keeps each wave's load count small (its
+//    waits stay exact) and puts thousands of waves in flight even for
+//    2560-row outputs.  Every weight load of a wave is issued before any
+//    arithmetic and consumed in issue order.
+//  * Each wave stages the activations of its own K slice into private LDS,
+//    laid out per pair (36 dwords: 32 bf16 pairs + two block biases) so that
+//    the eight columns of a wave hit distinct LDS banks.
+//  * Dequantisation happens in registers without converting nibbles to
+//    float: v_perm_b32 splices each nibble under the byte 0x43, which makes
+//    the bf16 value 128 + nibble, and v_dot2c_f32_bf16 multiplies two of them
+//    with two activations.  Per block, sum x*(128+n) - 136*sum(x) equals
+//    sum x*(n-8); the -136*sum(x) bias depends on x only and is computed once
+//    during staging.  The block sum is scaled by d in fp32, and the 8 lanes
+//    of a row are reduced with DPP.
+#include "smx_common.h"
+
+namespace smx {
+namespace {
+
+constexpr uint32_t kNib = 0x0F0F0F0Fu;
+constexpr uint32_t kMagic = 0x43434343u;   // high byte of bf16 128.0
+constexpr uint32_t kSel01 = 0x04010400u;   // [b0, 0x43, b1, 0x43]
+constexpr uint32_t kSel23 = 0x04030402u;   // [b2, 0x43, b3, 0x43]
+constexpr uint32_t kOnes = 0x3F803F80u;    // bf16 pair (1.0, 1.0)
+
+// acc += sum over the 8 nibbles of word w of x * (128 + nibble).
+// The low nibbles of bytes (0,1) pair with activation dword xl01, bytes
+// (2,3) with xl23; the high nibbles with xh01 and xh23.
+__device__ __forceinline__ float word_dot(uint32_t w, uint32_t xl01, uint32_t xl23,
+                                          uint32_t xh01, uint32_t xh23, float acc) {
+  const uint32_t l = w & kNib;
+  const uint32_t h = (w >> 4) & kNib;
+  acc = dot2_bf16(perm_b32(kMagic, l, kSel01), xl01, acc);
+  acc = dot2_bf16(perm_b32(kMagic, l, kSel23), xl23, acc);
+  acc = dot2_bf16(perm_b32(kMagic, h, kSel01), xh01, acc);
+  acc = dot2_bf16(perm_b32(kMagic, h, kSel23), xh23, acc);
+  return acc;
+}
+
+struct Pair {
+  u32x4 a;     // bytes 0..15  : d_even, qs_even[0..13]
+  u32x4 b;     // bytes 16..31 : qs_even[14..15], d_odd, qs_odd[0..11]
+  uint32_t c;  // bytes 32..35 : qs_odd[12..15]
+};
+
+__device__ __forceinline__ Pair load_pair(const uint8_t* p) {
+  Pair r;
+  r.a = *reinterpret_cast<const u32x4_a4*>(p);
+  r.b = *reinterpret_cast<const u32x4_a4*>(p + 16);
+  r.c = *reinterpret_cast<const uint32_t*>(p + 32);
+  return r;
+}
+
+// Dot product of one block pair with its staged activations.
+// xs points at the pair's 36-dword LDS record: even-block x (16 dwords),
+// odd-block x (16 dwords), bias_even, bias_odd.
+__device__ __forceinline__ float pair_dot(const Pair& w, const u32x4* xs, float acc) {
+  const u32x4 x0 = xs[0], x1 = xs[1], x2 = xs[2], x3 = xs[3];
+  const u32x4 y0 = xs[4], y1 = xs[5], y2 = xs[6], y3 = xs[7];
+  const u32x2 bias = *reinterpret_cast<const u32x2*>(xs + 8);
+  // Even block: its first and last two qs bytes straddle a.x and b.x.
+  const uint32_t e0 = (w.a.x & 0xffff0000u) | (w.b.x & 0x0000ffffu);  // qs 14,15,0,1
+  float se = __uint_as_float(bias.x);
+  se = word_dot(e0, x1.w, x0.x, x3.w, x2.x, se);     // (14,15)->x7,x15 (0,1)->x0,x8
+  se = word_dot(w.a.y, x0.y, x0.z, x2.y, x2.z, se);  // (2,3)->x1,x9 (4,5)->x2,x10
+  se = word_dot(w.a.z, x0.w, x1.x, x2.w, x3.x, se);  // (6,7)->x3,x11 (8,9)->x4,x12
+  se = word_dot(w.a.w, x1.y, x1.z, x3.y, x3.z, se);  // (10,11)->x5,x13 (12,13)->x6,x14
+  float so = __uint_as_float(bias.y);
+  so = word_dot(w.b.y, y0.x, y0.y, y2.x, y2.y, so);
+  so = word_dot(w.b.z, y0.z, y0.w, y2.z, y2.w, so);
+  so = word_dot(w.b.w, y1.x, y1.y, y3.x, y3.y, so);
+  so = word_dot(w.c, y1.z, y1.w, y3.z, y3.w, so);
+  const float de = f16_bits_to_f32(w.a.x & 0xffffu);
+  const float dd = f16_bits_to_f32(w.b.x >> 16);
+  acc = fmaf(de, se, acc);
+  acc = fmaf(dd, so, acc);
+  return acc;
+}
+
+// One workgroup owns RG groups of 8 weight rows.  Its waves split the K
+// dimension: pair group g (pairs 8g..8g+7) belongs to wave g % ks, and lane
+// 8r+c of a wave handles pair 8g+c of row r.  Each wave stages only the
+// activations of its own pair groups into a private LDS slice, so no
+// workgroup barrier separates the weight loads from the arithmetic; the ks
+// partial sums of a row meet in LDS at the end.  SWIGLU: rows 0-3 of a group
+// are gate rows, rows 4-7 the matching up rows, and the output is
+// silu(gate) * up for 4 features per group.
+template <int NPMAX, int RG, bool SWIGLU>
+__global__ __launch_bounds__(512) void q4_0_gemv_kernel(
+    const uint16_t* __restrict__ x, const uint8_t* __restrict__ w,
+    uint16_t* __restrict__ y, int n_out, int npairs, int64_t up_offset_rows) {
+  extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+  const int ks = blockDim.x >> 6;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int col = lane & 7;
+  const int rsub = lane >> 3;
+  const int64_t row_bytes = (int64_t)npairs * 36;
+  const int nchunks = npairs * 8;
+  uint32_t* xs = lds + wave * (NPMAX * 8 * 36);
+  float* part = reinterpret_cast<float*>(lds + ks * (NPMAX * 8 * 36));
+
+  // 1. This wave's activation chunks (16 bytes each, one per lane per group).
+  u32x4 xv[NPMAX];
+  const u32x4* xg = reinterpret_cast<const u32x4*>(x);
+#pragma unroll
+  for (int t = 0; t < NPMAX; ++t) {
+    const int c = (wave + ks * t) * 64 + lane;
+    xv[t] = c < nchunks ? xg[c] : u32x4{0u, 0u, 0u, 0u};
+  }
+
+  // 2. Every weight load of this wave.
+  constexpr int OUT_PER_GROUP = SWIGLU ? 4 : 8;
+  int out_idx[RG];
+  int64_t wrow[RG];
+  bool row_ok[RG];
+#pragma unroll
+  for (int g = 0; g < RG; ++g) {
+    const int o = (blockIdx.x * RG + g) * OUT_PER_GROUP + (SWIGLU ? (rsub & 3) : rsub);
+    out_idx[g] = o;
+    row_ok[g] = o < n_out;
+    wrow[g] = SWIGLU ? (o + ((rsub >> 2) ? up_offset_rows : 0)) : o;
+  }
+  Pair wp[RG][NPMAX];
+#pragma unroll
+  for (int g = 0; g < RG; ++g) {
+#pragma unroll
+    for (int t = 0; t < NPMAX; ++t) {
+      const int j = (wave + ks * t) * 8 + col;
+      if (row_ok[g] && j < npairs) {
+        wp[g][t] = load_pair(w + wrow[g] * row_bytes + 36 * j);
+      } else {
+        wp[g][t].a = u32x4{0u, 0u, 0u, 0u};
+        wp[g][t].b = u32x4{0u, 0u, 0u, 0u};
+        wp[g][t].c = 0u;
+      }
+    }
+  }
+
+  // 3. Stage the activations as 36-dword pair records with the block biases
+  //    -136 * sum(x_block).  The four chunks of a block sit in one lane quad.
+#pragma unroll
+  for (int t = 0; t < NPMAX; ++t) {
+    const u32x4 v = xv[t];
+    float s = 0.f;
+    s = dot2_bf16(v.x, kOnes, s);
+    s = dot2_bf16(v.y, kOnes, s);
+    s = dot2_bf16(v.z, kOnes, s);
+    s = dot2_bf16(v.w, kOnes, s);
+    s = sum4(s);
+    uint32_t* rec = xs + (t * 8 + (lane >> 3)) * 36;
+    *reinterpret_cast<u32x4*>(rec + 4 * (lane & 7)) = v;
+    if ((lane & 3) == 0) rec[32 + ((lane >> 2) & 1)] = __float_as_uint(-136.0f * s);
+  }
+  // The slice is private to this wave: LDS operations of one wave complete
+  // in order, so only the compiler has to be kept from reordering.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+  // 4. Dot products, consuming the weights in issue order.
+  float acc[RG];
+#pragma unroll
+  for (int g = 0; g < RG; ++g) acc[g] = 0.f;
+#pragma unroll
+  for (int t = 0; t < NPMAX; ++t) {
+    const int j = (wave + ks * t) * 8 + col;
+    if (j < npairs) {
+      const u32x4* rec = reinterpret_cast<const u32x4*>(xs + (t * 8 + col) * 36);
+#pragma unroll
+      for (int g = 0; g < RG; ++g) acc[g] = pair_dot(wp[g][t], rec, acc[g]);
+    }
+  }
+
+  // 5. Row sums: 8 lanes by DPP, then the ks waves through LDS.
+#pragma unroll
+  for (int g = 0; g < RG; ++g) {
+    const float v = sum8(acc[g]);
+    if (col == 0) part[wave * (8 * RG) + g * 8 + rsub] = v;
+  }
+  __syncthreads();
+  if (wave == 0 && lane < 8 * RG) {
+    const int g = lane >> 3;
+    const int r = lane & 7;
+    float tot = 0.f;
+    for (int i = 0; i < ks; ++i) tot += part[i * (8 * RG) + lane];
+    if constexpr (SWIGLU) {
+      const int o = (blockIdx.x * RG + g) * 4 + r;
+      if (r < 4 && o < n_out) {
+        float up = 0.f;
+        for (int i = 0; i < ks; ++i) up += part[i * (8 * RG) + g * 8 + r + 4];
+        const float gb = round_bf16(tot);
+        const float ub = round_bf16(up);
+        y[o] = f32_to_bf16(gb / (1.0f + expf(-gb)) * ub);
+      }
+    } else {
+      const int o = (blockIdx.x * RG + g) * 8 + r;
+      if (o < n_out) y[o] = f32_to_bf16(tot);
+    }
+  }
+}
+
+// Any k % 32 == 0 and any 2-byte alignment: one wave per output row, lanes
+// stride over blocks.  Used for shapes the streaming kernel does not cover.
+template <bool SWIGLU>
+__global__ __launch_bounds__(64) void q4_0_gemv_generic_kernel(
+    const uint16_t* __restrict__ x, const uint8_t* __restrict__ w,
+    uint16_t* __restrict__ y, int n_out, int nblocks, int64_t up_offset_rows) {
+  const int o = blockIdx.x;
+  const int lane = threadIdx.x;
+  const int64_t row_bytes = (int64_t)nblocks * 18;
+  float acc[2] = {0.f, 0.f};
+#pragma unroll
+  for (int part = 0; part < (SWIGLU ? 2 : 1); ++part) {
+    const int64_t row = o + (part ? up_offset_rows : 0);
+    const uint16_t* wr = reinterpret_cast<const uint16_t*>(w + row * row_bytes);
+    float a = 0.f;
+    for (int b = lane; b < nblocks; b += 64) {
+      const uint16_t* blk = wr + 9 * b;
+      const float d = f16_bits_to_f32(blk[0]);
+      float s = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t two = blk[1 + i];  // qs[2i], qs[2i+1]
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint32_t byte = (two >> (8 * h)) & 0xffu;
+          const int jlo = 2 * i + h;
+          const float xl = bf16_bits_to_f32(x[32 * b + jlo]);
+          const float xh = bf16_bits_to_f32(x[32 * b + 16 + jlo]);
+          s = fmaf(xl, (float)((int)(byte & 15u) - 8), s);
+          s = fmaf(xh, (float)((int)(byte >> 4) - 8), s);
+        }
+      }
+      a = fmaf(d, s, a);
+    }
+    acc[part] = wave_sum(a);
+  }
+  if (lane == 0) {
+    if constexpr (SWIGLU) {
+      const float gb = round_bf16(acc[0]);
+      const float ub = round_bf16(acc[1]);
+      y[o] = f32_to_bf16(gb / (1.0f + expf(-gb)) * ub);
+    } else {
+      y[o] = f32_to_bf16(acc[0]);
+    }
+  }
+}
+
+// One thread per block: 32 bf16 = RNE(float(d) * (nibble - 8)), exact product.
+__global__ __launch_bounds__(256) void q4_0_dequant_kernel(
+    const uint8_t* __restrict__ w, uint16_t* __restrict__ out, int64_t total_blocks) {
+  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= total_blocks) return;
+  const uint16_t* blk = reinterpret_cast<const uint16_t*>(w + 18 * b);
+  const float d = f16_bits_to_f32(blk[0]);
+  uint32_t* o = reinterpret_cast<uint32_t*>(out + 32 * b);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t two = blk[1 + i];
+    const float l0 = d * (float)((int)(two & 15u) - 8);
+    const float l1 = d * (float)((int)((two >> 8) & 15u) - 8);
+    const float h0 = d * (float)((int)((two >> 4) & 15u) - 8);
+    const float h1 = d * (float)((int)((two >> 12) & 15u) - 8);
+    o[i] = pack_bf16x2(l0, l1);
+    o[8 + i] = pack_bf16x2(h0, h1);
+  }
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Host launchers.
+// ---------------------------------------------------------------------------
+
+template <int NPMAX, int RG, bool SWIGLU>
+static hipError_t launch_fast(hipStream_t s, const void* x, const void* w, void* y, int n_out,
+                              int npairs, int64_t up_rows, int ks) {
+  constexpr int OUT_PER_WG = (SWIGLU ? 4 : 8) * RG;
+  const int grid = (n_out + OUT_PER_WG - 1) / OUT_PER_WG;
+  const size_t lds = (size_t)ks * NPMAX * 8 * 36 * 4 + (size_t)ks * 8 * RG * 4;
+  hipLaunchKernelGGL((q4_0_gemv_kernel<NPMAX, RG, SWIGLU>), dim3(grid), dim3(64 * ks), lds, s,
+                     (const uint16_t*)x, (const uint8_t*)w, (uint16_t*)y, n_out, npairs,
+                     up_rows);
+  return hipGetLastError();
+}
+
+// Launch shape: rg row groups of 8 per workgroup, ks waves splitting K, np
+// pair groups per wave.  Aim for a few thousand waves with balanced slices.
+struct GemvShape {
+  int rg, ks, np;
+};
+
+static GemvShape pick_shape(int n_out, int out_per_group, int ngroups) {
+  GemvShape sh;
+  const int wgs1 = (n_out + out_per_group - 1) / out_per_group;
+  sh.rg = wgs1 >= 8192 ? 2 : 1;
+  const int wgs = (wgs1 + sh.rg - 1) / sh.rg;
+  // smallest np (<= 5 when possible) that still leaves >= 4 waves per SIMD
+  int np = 1;
+  while (np < ngroups && np < 5 && (long)wgs * ((ngroups + np - 1) / np) > 8192) ++np;
+  while ((ngroups + np - 1) / np > 8) ++np;
+  sh.np = np;
+  sh.ks = (ngroups + np - 1) / np;
+  const char* e = getenv("SMX_GEMV_SHAPE");  // "rg,ks" override for tuning sweeps
+  if (e) {
+    int a = 0, b = 0;
+    if (sscanf(e, "%d,%d", &a, &b) == 2 && (a == 1 || a == 2 || a == 4) && b >= 1 && b <= 8) {
+      sh.rg = a;
+      sh.ks = b < ngroups ? b : ngroups;
+      sh.np = (ngroups + sh.ks - 1) / sh.ks;
+    }
+  }
+  return sh;
+}
+
+template <int NPMAX, bool SWIGLU>
+static hipError_t dispatch_rg(hipStream_t s, const void* x, const void* w, void* y, int n_out,
+                              int npairs, int64_t up_rows, const GemvShape& sh) {
+  if (sh.rg == 4) return launch_fast<NPMAX, 4, SWIGLU>(s, x, w, y, n_out, npairs, up_rows, sh.ks);
+  if (sh.rg == 2) return launch_fast<NPMAX, 2, SWIGLU>(s, x, w, y, n_out, npairs, up_rows, sh.ks);
+  return launch_fast<NPMAX, 1, SWIGLU>(s, x, w, y, n_out, npairs, up_rows, sh.ks);
+}
+
+static hipError_t gemv_dispatch(hipStream_t s, const void* x, const void* w, void* y,
+                                int64_t n_out, int64_t k, bool swiglu) {
+  const int64_t nblocks = k / 32;
+  const int npairs = (int)(nblocks / 2);
+  const int ngroups = (npairs + 7) / 8;
+  const int64_t up_rows = swiglu ? n_out : 0;
+  GemvShape sh{1, 1, 1};
+  bool fast = (k % 64 == 0) && ((uintptr_t)w % 4 == 0) && ((uintptr_t)x % 16 == 0);
+  if (fast) {
+    sh = pick_shape((int)n_out, swiglu ? 4 : 8, ngroups);
+    fast = sh.np <= 8;
+  }
+  if (!fast) {
+    if (swiglu)
+      hipLaunchKernelGGL(q4_0_gemv_generic_kernel<true>, dim3((unsigned)n_out), dim3(64), 0, s,
+                         (const uint16_t*)x, (const uint8_t*)w, (uint16_t*)y, (int)n_out,
+                         (int)nblocks, up_rows);
+    else
+      hipLaunchKernelGGL(q4_0_gemv_generic_kernel<false>, dim3((unsigned)n_out), dim3(64), 0, s,
+                         (const uint16_t*)x, (const uint8_t*)w, (uint16_t*)y, (int)n_out,
+                         (int)nblocks, up_rows);
+    return hipGetLastError();
+  }
+#define SMX_NP_CASE(NPV)                                                                      \
+  case NPV:                                                                                   \
+    return swiglu ? dispatch_rg<NPV, true>(s, x, w, y, (int)n_out, npairs, up_rows, sh)       \
+                  : dispatch_rg<NPV, false>(s, x, w, y, (int)n_out, npairs, up_rows, sh);
+  switch (sh.np) {
+    SMX_NP_CASE(1)
+    SMX_NP_CASE(2)
+    SMX_NP_CASE(3)
+    SMX_NP_CASE(4)
+    SMX_NP_CASE(5)
+    SMX_NP_CASE(6)
+    SMX_NP_CASE(7)
+    SMX_NP_CASE(8)
+    default:
+      return hipErrorInvalidValue;
+  }
+#undef SMX_NP_CASE
+}
+
+}  // namespace smx
+
+#include "smx_abi_util.h"
+
+extern "C" int smx_q4_0_dequant_bf16(void* stream, const void* w, void* out, int64_t n,
+                                     int64_t k) {
+  SMX_REQUIRE(w && out, "w and out must be non-null");
+  SMX_REQUIRE(n >= 1 && k >= 32 && k % 32 == 0, "need n >= 1 and k a positive multiple of 32");
+  SMX_REQUIRE((uintptr_t)w % 2 == 0, "w must be 2-byte aligned");
+  SMX_REQUIRE((uintptr_t)out % 4 == 0, "out must be 4-byte aligned");
+  const int64_t total = n * (k / 32);
+  const int64_t grid = (total + 255) / 256;
+  SMX_REQUIRE(grid < (1ll << 31), "tensor too large");
+  hipLaunchKernelGGL(smx::q4_0_dequant_kernel, dim3((unsigned)grid), dim3(256), 0,
+                     (hipStream_t)stream, (const uint8_t*)w, (uint16_t*)out, total);
+  return (int)hipGetLastError();
+}
+
+extern "C" int smx_q4_0_gemv(void* stream, const void* x, const void* w, void* y, int64_t n,
+                             int64_t k) {
+  SMX_REQUIRE(x && w && y, "x, w and y must be non-null");
+  SMX_REQUIRE(n >= 1 && n < (1ll << 31), "n out of range");
+  SMX_REQUIRE(k >= 32 && k % 32 == 0 && k <= (1 << 20), "k must be a multiple of 32 in [32, 2^20]");
+  SMX_REQUIRE((uintptr_t)x % 2 == 0 && (uintptr_t)w % 2 == 0 && (uintptr_t)y % 2 == 0,
+              "x, w and y must be 2-byte aligned");
+  return (int)smx::gemv_dispatch((hipStream_t)stream, x, w, y, n, k, false);
+}
+
+extern "C" int smx_q4_0_gemv_swiglu(void* stream, const void* x, const void* w, void* out,
+                                    int64_t d, int64_t k) {
+  SMX_REQUIRE(x && w && out, "x, w and out must be non-null");
+  SMX_REQUIRE(d >= 1 && d < (1ll << 30), "d out of range");
+  SMX_REQUIRE(k >= 32 && k % 32 == 0 && k <= (1 << 20), "k must be a multiple of 32 in [32, 2^20]");
+  SMX_REQUIRE((uintptr_t)x % 2 == 0 && (uintptr_t)w % 2 == 0 && (uintptr_t)out % 2 == 0,
+              "x, w and out must be 2-byte aligned");
+  return (int)smx::gemv_dispatch((hipStream_t)stream, x, w, out, d, k, true);
+}

@@ -1,0 +1,322 @@
+// The small fused ops around the GEMVs and attention of one decode step:
+// residual add + RMSNorm, per-head q/k RMSNorm + neox RoPE + paged KV write,
+// SwiGLU, embedding gather, greedy argmax and the on-device step advance.
+// Each is a few kilobytes of traffic; they are written to be launch- and
+// latency-cheap (one workgroup per row, vector loads, wave reductions).
+#include <math.h>
+
+#include "smx_common.h"
+
+namespace smx {
+namespace {
+
+// Block-wide sum for up to 1024 threads (wave sums, then LDS).
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nw = (blockDim.x + 63) >> 6;
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float t = 0.f;
+  for (int i = 0; i < nw; ++i) t += red[i];
+  __syncthreads();
+  return t;
+}
+
+// s = x + r (fp32); residual_out = bf16(s); y = bf16(s * inv_rms * gamma).
+// Follows norm_ub (src/spark_vllm_ascend/kernels/linear.py:202-224): the
+// normalised value uses the fp32 sum, not its bf16 rounding.  Each thread
+// owns 8-element chunks and writes only the indices it read, so
+// residual_out may alias residual.
+__global__ __launch_bounds__(256) void add_rmsnorm_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* residual, const uint16_t* __restrict__ gamma,
+    uint16_t* __restrict__ y, uint16_t* residual_out, int hidden, float eps) {
+  __shared__ float red[16];
+  const int64_t row = blockIdx.x;
+  const u32x4* xr = reinterpret_cast<const u32x4*>(x + row * hidden);
+  const u32x4* rr = residual ? reinterpret_cast<const u32x4*>(residual + row * hidden) : nullptr;
+  const int nch = hidden / 8;
+  constexpr int MAXC = 8;  // hidden <= 8 * 256 * MAXC
+  float sv[MAXC][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < MAXC; ++c) {
+    const int ch = threadIdx.x + c * 256;
+    if (ch < nch) {
+      const u32x4 a = xr[ch];
+      const u32x4 b = rr ? rr[ch] : u32x4{0u, 0u, 0u, 0u};
+      const uint32_t aw[4] = {a.x, a.y, a.z, a.w};
+      const uint32_t bw[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sv[c][2 * i] = bf16_lo(aw[i]) + bf16_lo(bw[i]);
+        sv[c][2 * i + 1] = bf16_hi(aw[i]) + bf16_hi(bw[i]);
+        ss += sv[c][2 * i] * sv[c][2 * i] + sv[c][2 * i + 1] * sv[c][2 * i + 1];
+      }
+    }
+  }
+  ss = block_sum(ss, red);
+  const float inv = 1.0f / sqrtf(ss / (float)hidden + eps);
+  const u32x4* gr = reinterpret_cast<const u32x4*>(gamma);
+#pragma unroll
+  for (int c = 0; c < MAXC; ++c) {
+    const int ch = threadIdx.x + c * 256;
+    if (ch < nch) {
+      const u32x4 g = gr[ch];
+      const uint32_t gw[4] = {g.x, g.y, g.z, g.w};
+      uint32_t yo[4], ro[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float s0 = sv[c][2 * i], s1 = sv[c][2 * i + 1];
+        ro[i] = pack_bf16x2(s0, s1);
+        yo[i] = pack_bf16x2(s0 * inv * bf16_lo(gw[i]), s1 * inv * bf16_hi(gw[i]));
+      }
+      reinterpret_cast<u32x4*>(y + row * hidden)[ch] = u32x4{yo[0], yo[1], yo[2], yo[3]};
+      if (residual_out)
+        reinterpret_cast<u32x4*>(residual_out + row * hidden)[ch] = u32x4{ro[0], ro[1], ro[2], ro[3]};
+    }
+  }
+}
+
+// One wave per (head, token).  head_dim = 128: lane i owns dims i and i + 64,
+// which are exactly a neox rotation pair.
+//   q heads : RMSNorm(q_gamma) -> RoPE -> q_out
+//   k heads : RMSNorm(k_gamma) -> RoPE -> k_cache[slot]
+//   v heads : copy -> v_cache[slot]
+// Norm outputs and rotated values are rounded to bf16 like the reference's
+// stage outputs (src/spark_vllm_ascend/kernels/qkv.py:179-189).
+__global__ __launch_bounds__(64) void qknorm_rope_kv_kernel(
+    const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ q_gamma,
+    const uint16_t* __restrict__ k_gamma, const uint16_t* __restrict__ cos_sin,
+    const int64_t* __restrict__ positions, const int64_t* __restrict__ slot_mapping,
+    uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache,
+    int n_q, int n_kv, int64_t cache_slots, int max_position, float eps) {
+  constexpr int HD = 128, HALF = 64;
+  const int h = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+  const int nh = n_q + 2 * n_kv;
+  const uint16_t* src = qkv + ((int64_t)t * nh + h) * HD;
+  float a = bf16_bits_to_f32(src[lane]);
+  float b = bf16_bits_to_f32(src[lane + HALF]);
+  const int64_t slot = slot_mapping[t];
+  const bool write_kv = slot >= 0 && slot < cache_slots;
+  if (h >= n_q + n_kv) {  // v head
+    if (write_kv) {
+      uint16_t* dst = v_cache + (slot * n_kv + (h - n_q - n_kv)) * HD;
+      dst[lane] = src[lane];
+      dst[lane + HALF] = src[lane + HALF];
+    }
+    return;
+  }
+  const uint16_t* gam = h < n_q ? q_gamma : k_gamma;
+  const float ss = wave_sum(a * a + b * b);
+  const float inv = 1.0f / sqrtf(ss / (float)HD + eps);
+  a = round_bf16(a * inv * bf16_bits_to_f32(gam[lane]));
+  b = round_bf16(b * inv * bf16_bits_to_f32(gam[lane + HALF]));
+  int64_t pos = positions[t];
+  pos = pos < 0 ? 0 : (pos >= max_position ? max_position - 1 : pos);
+  const uint16_t* cs = cos_sin + pos * HD;
+  const float c = bf16_bits_to_f32(cs[lane]);
+  const float s = bf16_bits_to_f32(cs[lane + HALF]);
+  const uint16_t u = f32_to_bf16(a * c - b * s);
+  const uint16_t v = f32_to_bf16(b * c + a * s);
+  if (h < n_q) {
+    uint16_t* dst = q_out + ((int64_t)t * n_q + h) * HD;
+    dst[lane] = u;
+    dst[lane + HALF] = v;
+  } else if (write_kv) {
+    uint16_t* dst = k_cache + (slot * n_kv + (h - n_q)) * HD;
+    dst[lane] = u;
+    dst[lane + HALF] = v;
+  }
+}
+
+// out = bf16(silu(g) * u) with silu(g) = g / (1 + exp(-g)), all in fp32.
+__global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restrict__ gu,
+                                                       uint16_t* __restrict__ out, int64_t rows,
+                                                       int64_t d) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= rows * d) return;
+  const int64_t r = i / d, c = i % d;
+  const float g = bf16_bits_to_f32(gu[r * 2 * d + c]);
+  const float u = bf16_bits_to_f32(gu[r * 2 * d + d + c]);
+  out[i] = f32_to_bf16(g / (1.0f + expf(-g)) * u);
+}
+
+__global__ __launch_bounds__(256) void embedding_kernel(const uint16_t* __restrict__ table,
+                                                        const int64_t* __restrict__ ids,
+                                                        uint16_t* __restrict__ out, int64_t vocab,
+                                                        int64_t hidden) {
+  const int64_t t = blockIdx.y;
+  const int64_t id = ids[t];
+  const bool ok = id >= 0 && id < vocab;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < hidden;
+       i += (int64_t)gridDim.x * blockDim.x)
+    out[t * hidden + i] = ok ? table[id * hidden + i] : (uint16_t)0;
+}
+
+// (value, index) ordering for argmax: larger value wins, NaN is largest,
+// ties go to the lower index.
+__device__ __forceinline__ bool better(float v, int64_t i, float bv, int64_t bi) {
+  const bool vn = v != v, bn = bv != bv;
+  if (vn != bn) return vn;
+  if (!vn && v != bv) return v > bv;
+  return i < bi;
+}
+
+// One 1024-thread workgroup per row.
+__global__ __launch_bounds__(1024) void argmax_kernel(const uint16_t* __restrict__ logits,
+                                                      int64_t vocab, int64_t* __restrict__ out) {
+  __shared__ float sv[16];
+  __shared__ int64_t si[16];
+  const int64_t row = blockIdx.x;
+  const uint16_t* lr = logits + row * vocab;
+  float bv = -INFINITY;
+  int64_t bi = INT64_MAX;
+  for (int64_t i = threadIdx.x; i < vocab; i += blockDim.x) {
+    const float v = bf16_bits_to_f32(lr[i]);
+    if (better(v, i, bv, bi)) {
+      bv = v;
+      bi = i;
+    }
+  }
+  // wave reduction with shuffles
+  for (int m = 32; m >= 1; m >>= 1) {
+    const float ov = __shfl_xor(bv, m, 64);
+    const int64_t oi = __shfl_xor(bi, m, 64);
+    if (better(ov, oi, bv, bi)) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) {
+    sv[wave] = bv;
+    si[wave] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int nw = blockDim.x >> 6;
+    for (int wv = 1; wv < nw; ++wv)
+      if (better(sv[wv], si[wv], bv, bi)) {
+        bv = sv[wv];
+        bi = si[wv];
+      }
+    out[row] = bi == INT64_MAX ? 0 : bi;
+  }
+}
+
+__global__ void decode_advance_kernel(const int64_t* __restrict__ next_ids, int64_t* ids,
+                                      int64_t* positions, int32_t* seq_lens,
+                                      int64_t* slot_mapping, const int32_t* block_table,
+                                      int64_t* tokens_out, int rows, int max_blocks,
+                                      int block_size, int max_len) {
+  const int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  const int64_t nid = next_ids[r];
+  const int64_t p = positions[r] + 1;
+  ids[r] = nid;
+  positions[r] = p;
+  seq_lens[r] = (int32_t)(p + 1);
+  const int64_t blk = p / block_size;
+  slot_mapping[r] =
+      blk < max_blocks ? (int64_t)block_table[(int64_t)r * max_blocks + blk] * block_size +
+                             p % block_size
+                       : -1;
+  if (tokens_out && p < max_len) tokens_out[(int64_t)r * max_len + p] = nid;
+}
+
+}  // namespace
+}  // namespace smx
+
+#include "smx_abi_util.h"
+
+extern "C" int smx_add_rmsnorm(void* stream, const void* x, const void* residual,
+                               const void* gamma, void* y, void* residual_out, int64_t rows,
+                               int64_t hidden, float eps) {
+  SMX_REQUIRE(x && gamma && y, "x, gamma and y must be non-null");
+  SMX_REQUIRE(rows >= 1 && rows < (1ll << 31), "rows out of range");
+  SMX_REQUIRE(hidden >= 8 && hidden % 8 == 0 && hidden <= 16384,
+              "hidden must be a multiple of 8 in [8, 16384]");
+  SMX_REQUIRE(eps >= 0.f && isfinite(eps), "eps must be finite and >= 0");
+  SMX_REQUIRE((uintptr_t)x % 16 == 0 && (uintptr_t)gamma % 16 == 0 && (uintptr_t)y % 16 == 0 &&
+                  (uintptr_t)residual % 16 == 0 && (uintptr_t)residual_out % 16 == 0,
+              "bf16 tensors must be 16-byte aligned");
+  hipLaunchKernelGGL(smx::add_rmsnorm_kernel, dim3((unsigned)rows), dim3(256), 0,
+                     (hipStream_t)stream, (const uint16_t*)x, (const uint16_t*)residual,
+                     (const uint16_t*)gamma, (uint16_t*)y, (uint16_t*)residual_out, (int)hidden,
+                     eps);
+  return (int)hipGetLastError();
+}
+
+extern "C" int smx_qknorm_rope_kv_write(void* stream, const void* qkv, const void* q_gamma,
+                                        const void* k_gamma, const void* cos_sin,
+                                        const int64_t* positions, const int64_t* slot_mapping,
+                                        void* q_out, void* k_cache, void* v_cache,
+                                        int32_t num_tokens, int32_t n_q, int32_t n_kv,
+                                        int32_t head_dim, int32_t num_blocks, int32_t block_size,
+                                        int32_t max_position, float eps) {
+  SMX_REQUIRE(qkv && q_gamma && k_gamma && cos_sin && positions && slot_mapping && q_out &&
+                  k_cache && v_cache,
+              "null pointer argument");
+  SMX_REQUIRE(head_dim == 128, "head_dim must be 128");
+  SMX_REQUIRE(num_tokens >= 1 && num_tokens <= 65535, "num_tokens must be in [1, 65535]");
+  SMX_REQUIRE(n_q >= 1 && n_kv >= 1 && n_q + 2 * n_kv <= 65535, "bad head counts");
+  SMX_REQUIRE(num_blocks >= 1 && block_size >= 1 && max_position >= 1,
+              "num_blocks, block_size and max_position must be >= 1");
+  SMX_REQUIRE(eps >= 0.f && isfinite(eps), "eps must be finite and >= 0");
+  SMX_REQUIRE((uintptr_t)positions % 8 == 0 && (uintptr_t)slot_mapping % 8 == 0,
+              "int64 arrays must be 8-byte aligned");
+  hipLaunchKernelGGL(smx::qknorm_rope_kv_kernel, dim3(n_q + 2 * n_kv, num_tokens), dim3(64), 0,
+                     (hipStream_t)stream, (const uint16_t*)qkv, (const uint16_t*)q_gamma,
+                     (const uint16_t*)k_gamma, (const uint16_t*)cos_sin, positions, slot_mapping,
+                     (uint16_t*)q_out, (uint16_t*)k_cache, (uint16_t*)v_cache, n_q, n_kv,
+                     (int64_t)num_blocks * block_size, max_position, eps);
+  return (int)hipGetLastError();
+}
+
+extern "C" int smx_silu_mul(void* stream, const void* gate_up, void* out, int64_t rows,
+                            int64_t d) {
+  SMX_REQUIRE(gate_up && out, "null pointer argument");
+  SMX_REQUIRE(rows >= 1 && d >= 1 && rows * d < (1ll << 40), "bad shape");
+  const int64_t grid = (rows * d + 255) / 256;
+  SMX_REQUIRE(grid < (1ll << 31), "tensor too large");
+  hipLaunchKernelGGL(smx::silu_mul_kernel, dim3((unsigned)grid), dim3(256), 0,
+                     (hipStream_t)stream, (const uint16_t*)gate_up, (uint16_t*)out, rows, d);
+  return (int)hipGetLastError();
+}
+
+extern "C" int smx_embedding(void* stream, const void* table, const int64_t* ids, void* out,
+                             int64_t num_tokens, int64_t vocab, int64_t hidden) {
+  SMX_REQUIRE(table && ids && out, "null pointer argument");
+  SMX_REQUIRE(num_tokens >= 1 && num_tokens <= 65535, "num_tokens must be in [1, 65535]");
+  SMX_REQUIRE(vocab >= 1 && hidden >= 1, "vocab and hidden must be >= 1");
+  SMX_REQUIRE((uintptr_t)ids % 8 == 0, "ids must be 8-byte aligned");
+  const unsigned gx = (unsigned)((hidden + 255) / 256 < 64 ? (hidden + 255) / 256 : 64);
+  hipLaunchKernelGGL(smx::embedding_kernel, dim3(gx, (unsigned)num_tokens), dim3(256), 0,
+                     (hipStream_t)stream, (const uint16_t*)table, ids, (uint16_t*)out, vocab,
+                     hidden);
+  return (int)hipGetLastError();
+}
+
+extern "C" int smx_argmax_bf16(void* stream, const void* logits, int64_t rows, int64_t vocab,
+                               int64_t* out_ids) {
+  SMX_REQUIRE(logits && out_ids, "null pointer argument");
+  SMX_REQUIRE(rows >= 1 && rows < (1ll << 31) && vocab >= 1, "bad shape");
+  SMX_REQUIRE((uintptr_t)out_ids % 8 == 0, "out_ids must be 8-byte aligned");
+  hipLaunchKernelGGL(smx::argmax_kernel, dim3((unsigned)rows), dim3(1024), 0,
+                     (hipStream_t)stream, (const uint16_t*)logits, vocab, out_ids);
+  return (int)hipGetLastError();
+}
+
+extern "C" int smx_decode_advance(void* stream, const int64_t* next_ids, int64_t* ids,
+                                  int64_t* positions, int32_t* seq_lens, int64_t* slot_mapping,
+                                  const int32_t* block_table, int64_t* tokens_out, int32_t rows,
+                                  int32_t max_blocks, int32_t block_size, int32_t max_len) {
+  SMX_REQUIRE(next_ids && ids && positions && seq_lens && slot_mapping && block_table,
+              "null pointer argument");
+  SMX_REQUIRE(rows >= 1 && max_blocks >= 1 && block_size >= 1 && max_len >= 0, "bad sizes");
+  hipLaunchKernelGGL(smx::decode_advance_kernel, dim3((rows + 63) / 64), dim3(64), 0,
+                     (hipStream_t)stream, next_ids, ids, positions, seq_lens, slot_mapping,
+                     block_table, tokens_out, rows, max_blocks, block_size, max_len);
+  return (int)hipGetLastError();
+}

@@ -1,0 +1,227 @@
+"""Torch-tensor wrappers over the C ABI (the role of the reference's
+TORCH_LIBRARY wrapper, src/spark_vllm_ascend/native/head/extension.cpp:6-14).
+
+Each wrapper checks device, dtype, contiguity and element counts before the
+call (raising ValueError, as TORCH_CHECK raises c10::Error), passes raw data
+pointers plus the current HIP stream of the tensor's device, and returns the
+output tensor.  Outputs can be passed in (``out=``) so that a captured graph
+reuses fixed buffers; otherwise they are freshly allocated, as the
+reference's custom ops do (src/spark_vllm_ascend/integration/head.py:8-9).
+"""
+from __future__ import annotations
+
+import torch
+
+from . import call
+
+BF16 = torch.bfloat16
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _need(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+def _check(t: torch.Tensor, name: str, dtype: torch.dtype, numel: int | None = None,
+           device: torch.device | None = None) -> None:
+    _need(isinstance(t, torch.Tensor), f"{name} must be a tensor")
+    _need(t.is_cuda, f"{name} must be on a GPU device")
+    _need(t.dtype == dtype, f"{name} must be {dtype}, got {t.dtype}")
+    _need(t.is_contiguous(), f"{name} must be contiguous")
+    if numel is not None:
+        _need(t.numel() == numel, f"{name} must have {numel} elements, got {t.numel()}")
+    if device is not None:
+        _need(t.device == device, f"{name} must be on {device}, got {t.device}")
+
+
+def q4_0_row_bytes(k: int) -> int:
+    """Bytes of one Q4_0 row of k weights (k/32 blocks of 18 bytes)."""
+    return k // 32 * 18
+
+
+def q4_0_dequant_bf16(w: torch.Tensor, n: int, k: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    _need(k % 32 == 0 and k > 0 and n > 0, "need n > 0 and k a positive multiple of 32")
+    _check(w, "w", torch.uint8, n * q4_0_row_bytes(k))
+    if out is None:
+        out = torch.empty((n, k), dtype=BF16, device=w.device)
+    _check(out, "out", BF16, n * k, w.device)
+    call("smx_q4_0_dequant_bf16", _stream(w), w.data_ptr(), out.data_ptr(), n, k)
+    return out
+
+
+def q4_0_gemv(x: torch.Tensor, w: torch.Tensor, n: int, k: int,
+              out: torch.Tensor | None = None) -> torch.Tensor:
+    _need(k % 32 == 0 and k > 0 and n > 0, "need n > 0 and k a positive multiple of 32")
+    _check(x, "x", BF16, k)
+    _check(w, "w", torch.uint8, n * q4_0_row_bytes(k), x.device)
+    if out is None:
+        out = torch.empty((1, n), dtype=BF16, device=x.device)
+    _check(out, "out", BF16, n, x.device)
+    call("smx_q4_0_gemv", _stream(x), x.data_ptr(), w.data_ptr(), out.data_ptr(), n, k)
+    return out
+
+
+def q4_0_gemv_swiglu(x: torch.Tensor, w: torch.Tensor, d: int, k: int,
+                     out: torch.Tensor | None = None) -> torch.Tensor:
+    _need(k % 32 == 0 and k > 0 and d > 0, "need d > 0 and k a positive multiple of 32")
+    _check(x, "x", BF16, k)
+    _check(w, "w", torch.uint8, 2 * d * q4_0_row_bytes(k), x.device)
+    if out is None:
+        out = torch.empty((1, d), dtype=BF16, device=x.device)
+    _check(out, "out", BF16, d, x.device)
+    call("smx_q4_0_gemv_swiglu", _stream(x), x.data_ptr(), w.data_ptr(), out.data_ptr(), d, k)
+    return out
+
+
+def splitkv_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                   block_table: torch.Tensor, seq_lens: torch.Tensor, num_splits: int,
+                   scale: float, partial_o: torch.Tensor | None = None,
+                   partial_lse: torch.Tensor | None = None):
+    """Split-KV partials.  q [S, n_q, 128]; caches [blocks, bs, n_kv, 128]."""
+    _need(q.dim() == 3 and k_cache.dim() == 4, "q must be [seqs, n_q, hd], caches 4-D")
+    num_seqs, n_q, hd = q.shape
+    num_blocks, bs, n_kv, hd2 = k_cache.shape
+    _need(hd == hd2, "head_dim mismatch between q and the cache")
+    _need(tuple(v_cache.shape) == tuple(k_cache.shape), "k_cache and v_cache shapes differ")
+    _check(q, "q", BF16)
+    _check(k_cache, "k_cache", BF16, device=q.device)
+    _check(v_cache, "v_cache", BF16, device=q.device)
+    _check(block_table, "block_table", torch.int32, device=q.device)
+    _need(block_table.dim() == 2 and block_table.shape[0] == num_seqs, "block_table must be [seqs, max_blocks]")
+    _check(seq_lens, "seq_lens", torch.int32, num_seqs, q.device)
+    if partial_o is None:
+        partial_o = torch.empty((num_seqs, num_splits, n_q, hd), dtype=torch.float32, device=q.device)
+    if partial_lse is None:
+        partial_lse = torch.empty((num_seqs, num_splits, n_q), dtype=torch.float32, device=q.device)
+    _check(partial_o, "partial_o", torch.float32, num_seqs * num_splits * n_q * hd, q.device)
+    _check(partial_lse, "partial_lse", torch.float32, num_seqs * num_splits * n_q, q.device)
+    call("smx_splitkv_decode", _stream(q), q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+         block_table.data_ptr(), seq_lens.data_ptr(), partial_o.data_ptr(), partial_lse.data_ptr(),
+         num_seqs, num_splits, block_table.shape[1], num_blocks, bs, n_q, n_kv, hd, float(scale))
+    return partial_o, partial_lse
+
+
+def lse_merge(partial_o: torch.Tensor, partial_lse: torch.Tensor,
+              out: torch.Tensor | None = None) -> torch.Tensor:
+    _need(partial_o.dim() == 4, "partial_o must be [seqs, splits, n_q, hd]")
+    num_seqs, num_splits, n_q, hd = partial_o.shape
+    _check(partial_o, "partial_o", torch.float32)
+    _check(partial_lse, "partial_lse", torch.float32, num_seqs * num_splits * n_q, partial_o.device)
+    if out is None:
+        out = torch.empty((num_seqs, n_q, hd), dtype=BF16, device=partial_o.device)
+    _check(out, "out", BF16, num_seqs * n_q * hd, partial_o.device)
+    call("smx_lse_merge", _stream(partial_o), partial_o.data_ptr(), partial_lse.data_ptr(),
+         out.data_ptr(), num_seqs, num_splits, n_q, hd)
+    return out
+
+
+def add_rmsnorm(x: torch.Tensor, residual: torch.Tensor | None, gamma: torch.Tensor, eps: float,
+                out: torch.Tensor | None = None, residual_out: torch.Tensor | None = None):
+    """Returns (y, residual_out).  With residual=None: y = RMSNorm(x), residual_out = x."""
+    _need(x.dim() >= 1, "x must have a hidden dimension")
+    hidden = x.shape[-1]
+    rows = x.numel() // hidden
+    _check(x, "x", BF16)
+    _check(gamma, "gamma", BF16, hidden, x.device)
+    if residual is not None:
+        _check(residual, "residual", BF16, x.numel(), x.device)
+    if out is None:
+        out = torch.empty_like(x)
+    _check(out, "out", BF16, x.numel(), x.device)
+    if residual is not None and residual_out is None:
+        residual_out = torch.empty_like(x)
+    if residual_out is not None:
+        _check(residual_out, "residual_out", BF16, x.numel(), x.device)
+    call("smx_add_rmsnorm", _stream(x), x.data_ptr(),
+         residual.data_ptr() if residual is not None else None, gamma.data_ptr(), out.data_ptr(),
+         residual_out.data_ptr() if residual_out is not None else None, rows, hidden, float(eps))
+    return out, (residual_out if residual is not None else x)
+
+
+def qknorm_rope_kv_write(qkv: torch.Tensor, q_gamma: torch.Tensor, k_gamma: torch.Tensor,
+                         cos_sin: torch.Tensor, positions: torch.Tensor, slot_mapping: torch.Tensor,
+                         k_cache: torch.Tensor, v_cache: torch.Tensor, n_q: int, n_kv: int,
+                         eps: float, q_out: torch.Tensor | None = None) -> torch.Tensor:
+    num_blocks, bs, n_kv2, hd = k_cache.shape
+    _need(n_kv2 == n_kv, "cache kv-head count mismatch")
+    num_tokens = positions.numel()
+    _check(qkv, "qkv", BF16, num_tokens * (n_q + 2 * n_kv) * hd)
+    _check(q_gamma, "q_gamma", BF16, hd, qkv.device)
+    _check(k_gamma, "k_gamma", BF16, hd, qkv.device)
+    _check(cos_sin, "cos_sin", BF16, device=qkv.device)
+    _need(cos_sin.dim() == 2 and cos_sin.shape[1] == hd, "cos_sin must be [max_position, head_dim]")
+    _check(positions, "positions", torch.int64, num_tokens, qkv.device)
+    _check(slot_mapping, "slot_mapping", torch.int64, num_tokens, qkv.device)
+    _check(k_cache, "k_cache", BF16, device=qkv.device)
+    _check(v_cache, "v_cache", BF16, device=qkv.device)
+    _need(tuple(v_cache.shape) == tuple(k_cache.shape), "k_cache and v_cache shapes differ")
+    if q_out is None:
+        q_out = torch.empty((num_tokens, n_q, hd), dtype=BF16, device=qkv.device)
+    _check(q_out, "q_out", BF16, num_tokens * n_q * hd, qkv.device)
+    call("smx_qknorm_rope_kv_write", _stream(qkv), qkv.data_ptr(), q_gamma.data_ptr(),
+         k_gamma.data_ptr(), cos_sin.data_ptr(), positions.data_ptr(), slot_mapping.data_ptr(),
+         q_out.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), num_tokens, n_q, n_kv, hd,
+         num_blocks, bs, cos_sin.shape[0], float(eps))
+    return q_out
+
+
+def silu_mul(gate_up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    _check(gate_up, "gate_up", BF16)
+    d2 = gate_up.shape[-1]
+    _need(d2 % 2 == 0, "last dimension must be even")
+    rows = gate_up.numel() // d2
+    if out is None:
+        out = torch.empty((*gate_up.shape[:-1], d2 // 2), dtype=BF16, device=gate_up.device)
+    _check(out, "out", BF16, rows * d2 // 2, gate_up.device)
+    call("smx_silu_mul", _stream(gate_up), gate_up.data_ptr(), out.data_ptr(), rows, d2 // 2)
+    return out
+
+
+def embedding(table: torch.Tensor, ids: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    _check(table, "table", BF16)
+    _need(table.dim() == 2, "table must be [vocab, hidden]")
+    _check(ids, "ids", torch.int64, device=table.device)
+    vocab, hidden = table.shape
+    if out is None:
+        out = torch.empty((ids.numel(), hidden), dtype=BF16, device=table.device)
+    _check(out, "out", BF16, ids.numel() * hidden, table.device)
+    call("smx_embedding", _stream(table), table.data_ptr(), ids.data_ptr(), out.data_ptr(),
+         ids.numel(), vocab, hidden)
+    return out
+
+
+def argmax(logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    _check(logits, "logits", BF16)
+    vocab = logits.shape[-1]
+    rows = logits.numel() // vocab
+    if out is None:
+        out = torch.empty((rows,), dtype=torch.int64, device=logits.device)
+    _check(out, "out", torch.int64, rows, logits.device)
+    call("smx_argmax_bf16", _stream(logits), logits.data_ptr(), rows, vocab, out.data_ptr())
+    return out
+
+
+def decode_advance(next_ids: torch.Tensor, ids: torch.Tensor, positions: torch.Tensor,
+                   seq_lens: torch.Tensor, slot_mapping: torch.Tensor, block_table: torch.Tensor,
+                   block_size: int, tokens_out: torch.Tensor | None = None) -> None:
+    rows = ids.numel()
+    _check(next_ids, "next_ids", torch.int64, rows)
+    _check(ids, "ids", torch.int64, rows, next_ids.device)
+    _check(positions, "positions", torch.int64, rows, next_ids.device)
+    _check(seq_lens, "seq_lens", torch.int32, rows, next_ids.device)
+    _check(slot_mapping, "slot_mapping", torch.int64, rows, next_ids.device)
+    _check(block_table, "block_table", torch.int32, device=next_ids.device)
+    _need(block_table.dim() == 2 and block_table.shape[0] == rows, "block_table must be [rows, max_blocks]")
+    max_len = 0
+    if tokens_out is not None:
+        _check(tokens_out, "tokens_out", torch.int64, device=next_ids.device)
+        _need(tokens_out.dim() == 2 and tokens_out.shape[0] == rows, "tokens_out must be [rows, max_len]")
+        max_len = tokens_out.shape[1]
+    call("smx_decode_advance", _stream(ids), next_ids.data_ptr(), ids.data_ptr(),
+         positions.data_ptr(), seq_lens.data_ptr(), slot_mapping.data_ptr(), block_table.data_ptr(),
+         tokens_out.data_ptr() if tokens_out is not None else None, rows, block_table.shape[1],
+         block_size, max_len)

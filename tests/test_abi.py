@@ -1,0 +1,75 @@
+"""CPU-only checks of the C ABI: the library loads, exports every function
+include/smx.h declares, reports its ABI version, and rejects invalid
+arguments with SMX_EINVAL before any GPU work (these calls never reach a
+kernel, so they run without a GPU)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from _util import pkg
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def declared_functions():
+    text = (ROOT / "include" / "smx.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(smx_\w+)\s*\(", text)))
+
+
+def test_header_declares_entry_points():
+    names = declared_functions()
+    assert "smx_q4_0_gemv" in names and "smx_splitkv_decode" in names
+    assert len(names) >= 12
+
+
+def test_library_exports_every_declared_symbol():
+    native = pkg("native")
+    lib = native.load()
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, f"not exported: {missing}"
+    assert lib.smx_abi_version() == native.ABI_VERSION
+
+
+def test_bindings_cover_header():
+    native = pkg("native")
+    declared = set(declared_functions()) - {"smx_last_error"}
+    assert declared == set(native.SIGNATURES), declared ^ set(native.SIGNATURES)
+
+
+@pytest.mark.parametrize("call,args", [
+    ("smx_q4_0_gemv", (None, None, None, None, 64, 256)),
+    ("smx_q4_0_gemv", (None, 16, 16, 16, 64, 255)),
+    ("smx_q4_0_gemv", (None, 16, 16, 16, 0, 256)),
+    ("smx_q4_0_gemv", (None, 17, 16, 16, 64, 256)),
+    ("smx_q4_0_gemv_swiglu", (None, 16, 16, 16, 64, 100)),
+    ("smx_q4_0_dequant_bf16", (None, 16, 16, 64, 33)),
+    ("smx_splitkv_decode", (None, 16, 16, 16, 16, 16, 16, 16, 1, 4, 8, 8, 128, 32, 8, 64, 0.1)),
+    ("smx_splitkv_decode", (None, 16, 16, 16, 16, 16, 16, 16, 1, 4, 8, 8, 128, 32, 16, 128, 0.1)),
+    ("smx_splitkv_decode", (None, 16, 16, 16, 16, 16, 16, 16, 1, 4, 8, 8, 96, 32, 8, 128, 0.1)),
+    ("smx_splitkv_decode", (None, 16, 16, 16, 16, 16, 16, 16, 1, 0, 8, 8, 128, 32, 8, 128, 0.1)),
+    ("smx_splitkv_decode", (None, 16, 16, 16, 16, 16, 16, 16, 1, 4, 8, 8, 128, 32, 8, 128, -1.0)),
+    ("smx_lse_merge", (None, 16, 16, 16, 1, 0, 32, 128)),
+    ("smx_add_rmsnorm", (None, 16, 16, 16, 16, 16, 1, 2561, 1e-6)),
+    ("smx_add_rmsnorm", (None, 16, 16, 16, 16, 16, 1, 32768, 1e-6)),
+    ("smx_add_rmsnorm", (None, 8, 16, 16, 16, 16, 1, 2560, 1e-6)),
+    ("smx_qknorm_rope_kv_write", (None, 16, 16, 16, 16, 16, 16, 16, 16, 16, 1, 32, 8, 64, 8, 128, 100, 1e-6)),
+    ("smx_silu_mul", (None, 16, 16, 0, 10)),
+    ("smx_embedding", (None, 16, 16, 16, 0, 10, 10)),
+    ("smx_argmax_bf16", (None, 16, 0, 10, 16)),
+    ("smx_decode_advance", (None, 16, 16, 16, 16, 16, 16, None, 0, 1, 1, 0)),
+])
+def test_invalid_arguments_rejected_on_host(call, args):
+    native = pkg("native")
+    lib = native.load()
+    rc = getattr(lib, call)(*args)
+    assert rc == native.SMX_EINVAL
+    assert lib.smx_last_error().decode().startswith(call)
+
+
+def test_call_raises_with_message():
+    native = pkg("native")
+    with pytest.raises(native.SmxError, match="k must be a multiple of 32"):
+        native.call("smx_q4_0_gemv", None, 16, 16, 16, 64, 100)

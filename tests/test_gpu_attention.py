@@ -1,0 +1,164 @@
+"""GPU parity of split-KV decode attention and the LSE merge, through the C
+ABI.  Bars: merged output within 2e-2 absolute of the float64 textbook
+attention (q, K, V ~ N(0,1), outputs are O(0.1)); per-split lse within 1e-3
+and partial outputs within 2e-2 of the oracle's restatement of the
+reference's online softmax."""
+import numpy as np
+import pytest
+
+from oracle import attention as oatt
+from oracle.bf16 import bf16_bits_to_f32
+
+from _util import bf16_dev, f32_of, pkg, randn_bf16
+
+pytestmark = pytest.mark.gpu
+
+N_Q, N_KV, HD = 32, 8, 128
+
+
+@pytest.fixture(scope="module")
+def dev():
+    import torch
+    return torch.device("cuda:0")
+
+
+@pytest.fixture(scope="module")
+def ops():
+    return pkg("native.torch_ops")
+
+
+def _case(rng, lengths, bs, extra_blocks=3):
+    """Random q and paged caches for several sequences with shuffled pages."""
+    need = [-(-L // bs) for L in lengths]
+    max_blocks = max(need) + 1
+    nblk = sum(need) + extra_blocks
+    perm = rng.permutation(nblk).astype(np.int32)
+    table = np.full((len(lengths), max_blocks), -7, dtype=np.int32)  # junk past the end
+    at = 0
+    for i, nb in enumerate(need):
+        table[i, :nb] = perm[at:at + nb]
+        at += nb
+    kc = randn_bf16(rng, (nblk, bs, N_KV, HD))
+    vc = randn_bf16(rng, (nblk, bs, N_KV, HD))
+    q = randn_bf16(rng, (len(lengths), N_Q, HD))
+    return q, kc, vc, table
+
+
+def _run(ops, dev, q, kc, vc, table, lengths, splits, scale):
+    import torch
+    po, pl = ops.splitkv_decode(bf16_dev(q, dev), bf16_dev(kc, dev), bf16_dev(vc, dev),
+                                torch.from_numpy(table).to(dev),
+                                torch.tensor(lengths, dtype=torch.int32, device=dev), splits, scale)
+    out = ops.lse_merge(po, pl)
+    return f32_of(out), po.cpu().numpy(), pl.cpu().numpy()
+
+
+@pytest.mark.parametrize("L", [1, 2, 31, 32, 33, 127, 128, 129, 300, 2048, 4096, 6144])
+@pytest.mark.parametrize("splits", [1, 4, 8, 16, 32])
+def test_splitkv_vs_fp64(ops, dev, L, splits):
+    if L > 2048 and splits in (1, 4) and L != 6144:
+        pytest.skip("covered by other split counts")
+    rng = np.random.default_rng(L * 31 + splits)
+    bs = 128
+    q, kc, vc, table = _case(rng, [L], bs)
+    scale = HD ** -0.5
+    out, po, pl = _run(ops, dev, q, kc, vc, table, [L], splits, scale)
+    qf, kf, vf = (bf16_bits_to_f32(a) for a in (q, kc, vc))
+    k = oatt.gather_paged(kf, table[0], L)
+    v = oatt.gather_paged(vf, table[0], L)
+    ref = oatt.attention_f64(qf[0], k, v, scale)
+    err = np.max(np.abs(out.reshape(N_Q, HD) - ref))
+    assert err < 2e-2, f"merged output err {err}"
+    # per-split partials against the oracle's online softmax
+    bounds = oatt.split_bounds(L, splits)
+    opo, opl = oatt.splitkv_partials(qf[0], k, v, scale, bounds)
+    finite = np.isfinite(opl)
+    np.testing.assert_array_equal(np.isfinite(pl[0]), finite)
+    assert np.max(np.abs(pl[0][finite] - opl[finite]), initial=0) < 1e-3
+    assert np.max(np.abs(po[0][finite] - opo[finite]), initial=0) < 2e-2
+    assert np.all(po[0][~finite] == 0)
+
+
+@pytest.mark.parametrize("bs", [32, 64, 256])
+def test_block_sizes(ops, dev, bs):
+    rng = np.random.default_rng(bs)
+    L = 1000
+    q, kc, vc, table = _case(rng, [L], bs)
+    scale = HD ** -0.5
+    out, _, _ = _run(ops, dev, q, kc, vc, table, [L], 8, scale)
+    qf, kf, vf = (bf16_bits_to_f32(a) for a in (q, kc, vc))
+    ref = oatt.attention_f64(qf[0], oatt.gather_paged(kf, table[0], L),
+                             oatt.gather_paged(vf, table[0], L), scale)
+    assert np.max(np.abs(out.reshape(N_Q, HD) - ref)) < 2e-2
+
+
+def test_ragged_batch(ops, dev):
+    rng = np.random.default_rng(5)
+    lengths = [512, 3000, 77, 32768 // 4, 1]
+    bs = 128
+    q, kc, vc, table = _case(rng, lengths, bs)
+    scale = HD ** -0.5
+    out, _, _ = _run(ops, dev, q, kc, vc, table, lengths, 16, scale)
+    qf, kf, vf = (bf16_bits_to_f32(a) for a in (q, kc, vc))
+    out = out.reshape(len(lengths), N_Q, HD)
+    for i, L in enumerate(lengths):
+        ref = oatt.attention_f64(qf[i], oatt.gather_paged(kf, table[i], L),
+                                 oatt.gather_paged(vf, table[i], L), scale)
+        assert np.max(np.abs(out[i] - ref)) < 2e-2, f"sequence {i} (L={L})"
+
+
+def test_page_permutation_invariance(ops, dev):
+    """Same logical KV behind two different page orders gives the same bits."""
+    import torch
+    rng = np.random.default_rng(8)
+    L, bs = 1500, 128
+    q, kc, vc, table = _case(rng, [L], bs, extra_blocks=0)
+    nb = -(-L // bs)
+    perm = rng.permutation(kc.shape[0])
+    inv = np.argsort(perm)
+    kc2, vc2 = kc[perm], vc[perm]
+    table2 = table.copy()
+    table2[0, :nb] = inv[table[0, :nb]]
+    a, _, _ = _run(ops, dev, q, kc, vc, table, [L], 8, HD ** -0.5)
+    b, _, _ = _run(ops, dev, q, kc2, vc2, table2, [L], 8, HD ** -0.5)
+    np.testing.assert_array_equal(a, b)
+
+
+def test_equal_keys_give_mean_of_values(ops, dev):
+    rng = np.random.default_rng(2)
+    L, bs = 640, 128
+    q, kc, vc, table = _case(rng, [L], bs)
+    kc[:] = kc[0:1, 0:1]  # every key identical
+    out, _, _ = _run(ops, dev, q, kc, vc, table, [L], 4, HD ** -0.5)
+    vf = oatt.gather_paged(bf16_bits_to_f32(vc), table[0], L)
+    ref = np.repeat(vf.mean(axis=0), N_Q // N_KV, axis=0)
+    assert np.max(np.abs(out.reshape(N_Q, HD) - ref)) < 1e-2
+
+
+def test_bad_block_table_entry_poisons_only(ops, dev):
+    """An out-of-range page id is never dereferenced; the output is NaN."""
+    rng = np.random.default_rng(4)
+    L, bs = 400, 128
+    q, kc, vc, table = _case(rng, [L], bs)
+    table[0, 1] = 1 << 20
+    out, _, pl = _run(ops, dev, q, kc, vc, table, [L], 1, HD ** -0.5)
+    assert np.isnan(out).all()
+
+
+def test_partial_sentinels(ops, dev):
+    """Kernel writes stay inside partial_o / partial_lse."""
+    import torch
+    rng = np.random.default_rng(6)
+    L, bs, S = 700, 128, 8
+    q, kc, vc, table = _case(rng, [L], bs)
+    guard_o = torch.full((S * N_Q * HD + 64,), 17.0, device=dev)
+    guard_l = torch.full((S * N_Q + 64,), 17.0, device=dev)
+    po = guard_o[32:32 + S * N_Q * HD].view(1, S, N_Q, HD)
+    pl = guard_l[32:32 + S * N_Q].view(1, S, N_Q)
+    ops.splitkv_decode(bf16_dev(q, dev), bf16_dev(kc, dev), bf16_dev(vc, dev),
+                       torch.from_numpy(table).to(dev),
+                       torch.tensor([L], dtype=torch.int32, device=dev), S, HD ** -0.5,
+                       partial_o=po, partial_lse=pl)
+    go, gl = guard_o.cpu().numpy(), guard_l.cpu().numpy()
+    assert np.all(go[:32] == 17) and np.all(go[-32:] == 17)
+    assert np.all(gl[:32] == 17) and np.all(gl[-32:] == 17)
