@@ -93,9 +93,12 @@ int smx_q4_0_gemv_swiglu(void* stream, const void* x, const void* w,
  *   partial_o: [num_seqs, num_splits, n_q, head_dim] fp32 (normalised)
  *   partial_lse: [num_seqs, num_splits, n_q] fp32 (natural log; -inf for an
  *     empty split)
- * Split s of a sequence of length L covers tokens
- *   [s*T, min(L, (s+1)*T)), T = 32 * ceil(ceil(L / num_splits) / 32),
- * where L = min(seq_lens[r], max_blocks * block_size).
+ * Split s of a sequence covers tokens [s*T, min(L, (s+1)*T)) with
+ *   C = max_blocks * block_size (the block table's capacity),
+ *   T = 32 * ceil(ceil(C / num_splits) / 32), L = min(seq_lens[r], C);
+ * a split past L is empty (lse -inf, partial 0).  Deriving T from C rather
+ * than from the device-side length lets the kernel issue its page lookups
+ * before the length arrives.
  * Scores are q.k * scale in fp32; probabilities are rounded to bf16 before
  * they multiply V, and the running sum uses the unrounded fp32 values.
  * A block-table entry outside [0, num_blocks) is never dereferenced; the
@@ -113,9 +116,22 @@ int smx_splitkv_decode(void* stream, const void* q, const void* k_cache,
                        int32_t n_kv, int32_t head_dim, float scale);
 
 /*
+ * smx_splitkv_decode followed by smx_lse_merge on the same stream, in one
+ * call: out ([num_seqs, n_q, head_dim] bf16) receives the merged attention;
+ * partial_o / partial_lse are the workspace between the two launches.
+ */
+int smx_splitkv_decode_merged(void* stream, const void* q, const void* k_cache,
+                              const void* v_cache, const int32_t* block_table,
+                              const int32_t* seq_lens, float* partial_o,
+                              float* partial_lse, void* out, int32_t num_seqs,
+                              int32_t num_splits, int32_t max_blocks,
+                              int32_t num_blocks, int32_t block_size, int32_t n_q,
+                              int32_t n_kv, int32_t head_dim, float scale);
+
+/*
  * Log-sum-exp merge of the split partials:
  *   w_s = exp(lse_s - max_s lse) / sum, out = RNE_bf16(sum_s w_s * o_s).
- * out: [num_seqs, n_q, head_dim] bf16.
+ * out: [num_seqs, n_q, head_dim] bf16.  Requires head_dim == 128.
  * Replaces merge_attention (src/spark_vllm_ascend/kernels/vector.py:45-83)
  * without the reference model's sigmoid output gate.
  */
@@ -187,18 +203,37 @@ int smx_argmax_bf16(void* stream, const void* logits, int64_t rows,
                     int64_t vocab, int64_t* out_ids);
 
 /*
+ * Paged KV write (vLLM reshape_and_cache): for each token t with
+ * slot_mapping[t] in [0, num_blocks * block_size), copy key[t] and value[t]
+ * ([n_kv, head_dim] bf16 each) into k_cache / v_cache at that slot;
+ * slot -1 is skipped.  Replaces the cache stores of FusedQkvStage.store8
+ * (src/spark_vllm_ascend/kernels/qkv.py:192-198,226-236).
+ */
+int smx_reshape_and_cache(void* stream, const void* key, const void* value,
+                          void* k_cache, void* v_cache,
+                          const int64_t* slot_mapping, int32_t num_tokens,
+                          int32_t n_kv, int32_t head_dim, int32_t num_blocks,
+                          int32_t block_size);
+
+/*
  * Advance a decode batch by one token, on the device, so that one captured
- * graph serves every step:
- *   ids[r] = next_ids[r]; positions[r] += 1; seq_lens[r] = positions[r] + 1;
+ * graph serves every step (prompt ingestion and generation):
+ *   p = positions[r] + 1;
+ *   ids[r] = forced_ids[r, p] if forced_ids != NULL and p < forced_len[r]
+ *            else next_ids[r];
+ *   positions[r] = p; seq_lens[r] = p + 1;
  *   slot_mapping[r] = block_table[r, p / block_size] * block_size
- *                     + p % block_size  (p = new position; -1 when the
- *                     table has no entry for p);
- *   tokens_out[r, p] = next_ids[r] when tokens_out != NULL and p < max_len.
- * The slot formula is the reference's slot mapping
+ *                     + p % block_size  (-1 when the table has no entry);
+ *   tokens_out[r, p] = ids[r] when tokens_out != NULL and p < max_len.
+ * forced_ids is [rows, max_len] and forced_len an int32 [rows] device array
+ * (both NULL when no tokens are forced); keeping the forced length in device
+ * memory lets one graph switch from prompt to generated tokens.  The slot
+ * formula is the reference's slot mapping
  * (src/spark_vllm_ascend/integration/slot_mapping.py:8-33).
  */
-int smx_decode_advance(void* stream, const int64_t* next_ids, int64_t* ids,
-                       int64_t* positions, int32_t* seq_lens,
+int smx_decode_advance(void* stream, const int64_t* next_ids,
+                       const int64_t* forced_ids, const int32_t* forced_len,
+                       int64_t* ids, int64_t* positions, int32_t* seq_lens,
                        int64_t* slot_mapping, const int32_t* block_table,
                        int64_t* tokens_out, int32_t rows, int32_t max_blocks,
                        int32_t block_size, int32_t max_len);

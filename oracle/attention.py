@@ -47,11 +47,14 @@ def attention_f64(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float) -> 
     return out
 
 
-def split_bounds(length: int, num_splits: int, align: int = 32):
-    """Token range of each split: T = align * ceil(ceil(L / S) / align)."""
-    per = -(-length // num_splits)
+def split_bounds(length: int, num_splits: int, capacity: int | None = None, align: int = 32):
+    """Token range of each split: T = align * ceil(ceil(C / S) / align) where
+    C is the block table's capacity (default: the length itself); ranges are
+    clipped to the length, so splits past it are empty."""
+    cap = length if capacity is None else capacity
+    per = -(-cap // num_splits)
     t = -(-per // align) * align
-    return [(s * t, min(length, (s + 1) * t)) for s in range(num_splits)]
+    return [(min(length, s * t), min(length, (s + 1) * t)) for s in range(num_splits)]
 
 
 def splitkv_partials(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float,
@@ -97,8 +100,10 @@ def lse_merge(po: np.ndarray, pl: np.ndarray) -> np.ndarray:
 
 
 def splitkv_decode(q, k_cache, v_cache, table, length, num_splits, scale, tile=128):
-    """Paged convenience wrapper: gather, split, merge."""
+    """Paged convenience wrapper: gather, split (over the table's capacity),
+    merge."""
     k = gather_paged(k_cache, table, length)
     v = gather_paged(v_cache, table, length)
-    po, pl = splitkv_partials(q, k, v, scale, split_bounds(length, num_splits), tile)
+    cap = len(table) * k_cache.shape[1]
+    po, pl = splitkv_partials(q, k, v, scale, split_bounds(length, num_splits, cap), tile)
     return lse_merge(po, pl), po, pl

@@ -103,6 +103,7 @@ void oracle_q4_0_dequant_bf16(const uint8_t* blocks, int64_t n, int64_t k, uint1
 void oracle_q4_0_gemv_f64(const uint16_t* x, const uint8_t* blocks, int64_t n, int64_t k,
                           double* y) {
   const int64_t nb = k / 32;
+#pragma omp parallel for schedule(static)
   for (int64_t r = 0; r < n; ++r) {
     double acc = 0.0;
     for (int64_t b = 0; b < nb; ++b) {

@@ -1,0 +1,126 @@
+"""Q4_0 linear quant method: the plugin's operator surface for the GEMVs.
+
+The reference swaps a layer's ``quant_method`` for a class whose
+``apply(layer, x, bias=None)`` serves the fast path for batch-1 bf16 input
+and defers to the stock method otherwise (Q6HeadMethod,
+src/spark_vllm_ascend/integration/head.py:12-16,31).  This module offers the
+same hook for Q4_0 linears on vLLM's LinearMethodBase contract:
+
+  create_weights(layer, input_size_per_partition, output_partition_sizes,
+                 input_size, output_size, params_dtype, **extra)
+      registers ``layer.qweight``: uint8 [sum(output_partition_sizes),
+      input_size_per_partition/32*18], GGUF Q4_0 blocks as stored in the file.
+  process_weights_after_loading(layer)
+      validates the loaded blocks; the kernels stream GGUF blocks directly,
+      so no repack happens.
+  apply(layer, x, bias=None) -> [..., N] bf16
+      Q4_0 GEMV per activation row (HIP kernel), bias added after.
+
+vLLM is not installed in this image; when it is, the class derives from its
+LinearMethodBase so vLLM's loaders accept it unchanged.
+"""
+from __future__ import annotations
+
+import torch
+
+from ..native import torch_ops
+from .weights import row_bytes
+
+try:  # pragma: no cover - vLLM is absent here
+    from vllm.model_executor.layers.linear import LinearMethodBase as _Base
+except Exception:  # noqa: BLE001
+    class _Base:  # minimal stand-in with vLLM's method names
+        def create_weights(self, layer, *args, **kwargs):
+            raise NotImplementedError
+
+        def apply(self, layer, x, bias=None):
+            raise NotImplementedError
+
+        def process_weights_after_loading(self, layer):
+            return None
+
+
+class Q4_0Config:
+    """Quantization config naming the method, as vLLM's QuantizationConfig."""
+
+    @classmethod
+    def get_name(cls) -> str:
+        return "q4_0"
+
+    @classmethod
+    def get_supported_act_dtypes(cls):
+        return [torch.bfloat16]
+
+    def get_quant_method(self, layer, prefix: str = ""):
+        return Q4_0LinearMethod()
+
+
+class Q4_0LinearMethod(_Base):
+    """Q4_0 weights, bf16 activations, fp32 accumulation, bf16 output."""
+
+    def create_weights(self, layer: torch.nn.Module, input_size_per_partition: int,
+                       output_partition_sizes: list[int], input_size: int, output_size: int,
+                       params_dtype: torch.dtype, **extra_weight_attrs) -> None:
+        k = int(input_size_per_partition)
+        n = int(sum(output_partition_sizes))
+        if params_dtype not in (torch.bfloat16,):
+            raise ValueError(f"Q4_0 linears take bf16 activations, got {params_dtype}")
+        device = extra_weight_attrs.pop("device", None)
+        qweight = torch.nn.Parameter(
+            torch.empty((n, row_bytes(k)), dtype=torch.uint8, device=device), requires_grad=False)
+        layer.register_parameter("qweight", qweight)
+        layer.q4_0_n = n
+        layer.q4_0_k = k
+        layer.output_partition_sizes = list(output_partition_sizes)
+        for key, val in extra_weight_attrs.items():
+            setattr(qweight, key, val)
+
+    def process_weights_after_loading(self, layer: torch.nn.Module) -> None:
+        w = layer.qweight
+        if w.dtype != torch.uint8 or tuple(w.shape) != (layer.q4_0_n, row_bytes(layer.q4_0_k)):
+            raise ValueError(f"qweight must be uint8 {(layer.q4_0_n, row_bytes(layer.q4_0_k))}, "
+                             f"got {w.dtype} {tuple(w.shape)}")
+        if not w.is_contiguous():
+            layer.qweight = torch.nn.Parameter(w.contiguous(), requires_grad=False)
+
+    def apply(self, layer: torch.nn.Module, x: torch.Tensor,
+              bias: torch.Tensor | None = None) -> torch.Tensor:
+        n, k = layer.q4_0_n, layer.q4_0_k
+        if x.shape[-1] != k:
+            raise ValueError(f"expected last dim {k}, got {x.shape[-1]}")
+        if x.dtype != torch.bfloat16:
+            raise ValueError(f"expected bf16 activations, got {x.dtype}")
+        rows = x.reshape(-1, k).contiguous()
+        out = torch.empty((rows.shape[0], n), dtype=torch.bfloat16, device=x.device)
+        w = layer.qweight.reshape(-1)
+        for i in range(rows.shape[0]):
+            torch_ops.q4_0_gemv(rows[i], w, n, k, out=out[i])
+        out = out.reshape(*x.shape[:-1], n)
+        if bias is not None:
+            out = out + bias
+        return out
+
+    def apply_swiglu(self, layer: torch.nn.Module, x: torch.Tensor,
+                     out: torch.Tensor | None = None) -> torch.Tensor:
+        """Merged gate|up layer (two equal partitions): silu(gate) * up fused
+        into the GEMV epilogue, for one activation row."""
+        sizes = layer.output_partition_sizes
+        if len(sizes) != 2 or sizes[0] != sizes[1]:
+            raise ValueError("apply_swiglu needs a merged [gate, up] layer of equal halves")
+        return torch_ops.q4_0_gemv_swiglu(x.reshape(-1), layer.qweight.reshape(-1), sizes[0],
+                                          layer.q4_0_k, out=out)
+
+
+class Q4_0Linear(torch.nn.Module):
+    """A bare linear layer driven by Q4_0LinearMethod (used by the decode
+    model and tests in place of vLLM's parallel linear classes)."""
+
+    def __init__(self, input_size: int, output_partition_sizes: list[int], device=None):
+        super().__init__()
+        self.quant_method = Q4_0LinearMethod()
+        self.quant_method.create_weights(self, input_size, output_partition_sizes, input_size,
+                                         sum(output_partition_sizes), torch.bfloat16,
+                                         device=device)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self.quant_method.apply(self, x)

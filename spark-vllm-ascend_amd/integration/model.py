@@ -1,0 +1,263 @@
+"""Batch-1 decode of a Q4_0 decoder, one captured HIP graph per step.
+
+The reference replaces every decode step of every layer with one compiled
+kernel launch, ``layer_run(x, residual, positions, layer_name) -> (y,
+residual)`` (src/spark_vllm_ascend/integration/model.py:46-80), called by
+the model loop after the first input norm (src/spark_vllm_ascend/plugin/
+spark2_5.py:369-376), with the last layer's "next norm" being the model's
+final norm (integration/model.py:88-92).  vLLM captures the whole step in
+one device graph (src/tools/deployment/serve.py:34).
+
+Here one decode step is the kernel sequence
+
+  embedding -> RMSNorm(input_norm[0])
+  per layer:  QKV Q4_0 GEMV -> q/k RMSNorm + RoPE + KV write
+              -> split-KV attention -> LSE merge -> o_proj Q4_0 GEMV
+              -> add + RMSNorm(post_attention_norm)
+              -> gate|up Q4_0 GEMV with SwiGLU -> down Q4_0 GEMV
+              -> add + RMSNorm(next layer's input_norm or the final norm)
+  head Q4_0 GEMV -> argmax -> on-device advance (next input id, position,
+              sequence length, KV slot)
+
+captured once as a torch.cuda.CUDAGraph (a hipGraph).  Position, sequence
+length and slot are read from device memory by the kernels, as the
+reference reads them with load_bypass (src/spark_vllm_ascend/kernels/
+layer.py:52-53), so one graph serves every step; prompt tokens are fed
+through the same graph by the advance kernel's forced-id table.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+from ..native import torch_ops
+from .attention import choose_num_splits
+from .head import TiedQ4_0Head
+from .linear import Q4_0Linear
+from .weights import synthetic_q4_0
+
+
+@dataclass
+class DecoderConfig:
+    hidden: int = 2560
+    n_layers: int = 36
+    n_q: int = 32
+    n_kv: int = 8
+    head_dim: int = 128
+    intermediate: int = 9728
+    vocab: int = 151936
+    eps: float = 1e-6
+    rope_theta: float = 1e6
+    block_size: int = 128
+
+    @property
+    def qkv_rows(self) -> int:
+        return (self.n_q + 2 * self.n_kv) * self.head_dim
+
+
+def rope_cos_sin_cache(max_position: int, rot_dim: int, theta: float, device) -> torch.Tensor:
+    """vLLM's rotary table: inv_freq = theta^(-2i/d) in fp32, angles =
+    pos * inv_freq, rows cos | sin, cast to the model dtype (bf16)."""
+    inv_freq = 1.0 / (theta ** (torch.arange(0, rot_dim, 2, dtype=torch.float32) / rot_dim))
+    t = torch.arange(max_position, dtype=torch.float32)
+    freqs = torch.outer(t, inv_freq)
+    return torch.cat((freqs.cos(), freqs.sin()), dim=-1).to(torch.bfloat16).to(device)
+
+
+def _norm_weight(n: int, gen: torch.Generator, device) -> torch.Tensor:
+    return (1.0 + 0.1 * torch.randn(n, generator=gen, device=device)).to(torch.bfloat16)
+
+
+@dataclass
+class DecoderLayer:
+    qkv: Q4_0Linear
+    o_proj: Q4_0Linear
+    gate_up: Q4_0Linear
+    down: Q4_0Linear
+    input_norm: torch.Tensor
+    post_norm: torch.Tensor
+    q_norm: torch.Tensor
+    k_norm: torch.Tensor
+    kv_cache: torch.Tensor  # [2, num_blocks, block_size, n_kv, head_dim]
+    name: str = ""
+
+
+@dataclass
+class DecodeState:
+    """Device-resident step inputs (graph-invariant addresses)."""
+    ids: torch.Tensor            # int64 [1]
+    positions: torch.Tensor      # int64 [1]
+    seq_lens: torch.Tensor       # int32 [1]
+    slot_mapping: torch.Tensor   # int64 [1]
+    block_table: torch.Tensor    # int32 [1, max_blocks]
+    next_ids: torch.Tensor       # int64 [1]
+    forced: torch.Tensor         # int64 [1, max_len] prompt / teacher tokens
+    forced_len: torch.Tensor     # int32 [1]: positions below it take forced tokens
+    tokens: torch.Tensor         # int64 [1, max_len] every token fed, by position
+
+
+class DecodeModel:
+    """A batch-1 Q4_0 decoder with random-init weights of a given shape."""
+
+    def __init__(self, cfg: DecoderConfig, device, seed: int = 0, max_len: int = 8192,
+                 num_splits: int | None = None, weights: dict | None = None):
+        self.cfg = cfg
+        self.device = torch.device(device)
+        self.max_len = max_len
+        c = cfg
+        gen = torch.Generator(device=self.device)
+        gen.manual_seed(seed)
+        blocks_per_seq = -(-max_len // c.block_size)
+        self.num_blocks = blocks_per_seq + 1
+        self.layers: list[DecoderLayer] = []
+        for i in range(c.n_layers):
+            s = seed * 1000 + i * 10
+            qkv = Q4_0Linear(c.hidden, [c.n_q * c.head_dim, c.n_kv * c.head_dim,
+                                        c.n_kv * c.head_dim], device=self.device)
+            o_proj = Q4_0Linear(c.n_q * c.head_dim, [c.hidden], device=self.device)
+            gate_up = Q4_0Linear(c.hidden, [c.intermediate, c.intermediate], device=self.device)
+            down = Q4_0Linear(c.intermediate, [c.hidden], device=self.device)
+            for j, lin in enumerate((qkv, o_proj, gate_up, down)):
+                key = f"layers.{i}.{('qkv', 'o_proj', 'gate_up', 'down')[j]}"
+                if weights is not None and key in weights:
+                    lin.qweight.data.copy_(weights[key])
+                else:
+                    lin.qweight.data.copy_(synthetic_q4_0(lin.q4_0_n, lin.q4_0_k, s + j,
+                                                          self.device))
+                lin.quant_method.process_weights_after_loading(lin)
+            norms = []
+            for j, n in enumerate((c.hidden, c.hidden, c.head_dim, c.head_dim)):
+                key = f"layers.{i}.norm{j}"
+                norms.append(weights[key].to(self.device) if weights is not None and key in weights
+                             else _norm_weight(n, gen, self.device))
+            kv = torch.zeros((2, self.num_blocks, c.block_size, c.n_kv, c.head_dim),
+                             dtype=torch.bfloat16, device=self.device)
+            self.layers.append(DecoderLayer(qkv, o_proj, gate_up, down, *norms, kv_cache=kv,
+                                            name=f"model.layers.{i}.self_attn.attn"))
+        self.final_norm = (weights["final_norm"].to(self.device)
+                           if weights is not None and "final_norm" in weights
+                           else _norm_weight(c.hidden, gen, self.device))
+        head_blocks = (weights["head"] if weights is not None and "head" in weights
+                       else synthetic_q4_0(c.vocab, c.hidden, seed * 1000 + 999, self.device))
+        self.head = TiedQ4_0Head(head_blocks.to(self.device), c.vocab, c.hidden)
+        self.cos_sin = rope_cos_sin_cache(max_len, c.head_dim, c.rope_theta, self.device)
+        self.scale = 1.0 / math.sqrt(c.head_dim)
+        self.num_splits = num_splits or choose_num_splits(blocks_per_seq * c.block_size)
+
+        # pages are handed out in a seeded shuffled order, to exercise paging
+        perm = torch.randperm(self.num_blocks, generator=torch.Generator().manual_seed(seed))
+        table = perm[:blocks_per_seq].to(torch.int32).view(1, -1)
+        dev = self.device
+        self.state = DecodeState(
+            ids=torch.zeros(1, dtype=torch.int64, device=dev),
+            positions=torch.zeros(1, dtype=torch.int64, device=dev),
+            seq_lens=torch.ones(1, dtype=torch.int32, device=dev),
+            slot_mapping=torch.zeros(1, dtype=torch.int64, device=dev),
+            block_table=table.to(dev),
+            next_ids=torch.zeros(1, dtype=torch.int64, device=dev),
+            forced=torch.zeros((1, max_len), dtype=torch.int64, device=dev),
+            forced_len=torch.zeros(1, dtype=torch.int32, device=dev),
+            tokens=torch.full((1, max_len), -1, dtype=torch.int64, device=dev),
+        )
+        # activations (fixed addresses for graph capture)
+        bf = dict(dtype=torch.bfloat16, device=dev)
+        self.x = torch.empty((1, c.hidden), **bf)         # embedding / residual stream
+        self.h = torch.empty((1, c.hidden), **bf)         # normalised layer input
+        self.qkv_out = torch.empty((1, c.qkv_rows), **bf)
+        self.q = torch.empty((1, c.n_q, c.head_dim), **bf)
+        self.attn = torch.empty((1, c.n_q, c.head_dim), **bf)
+        self.o = torch.empty((1, c.hidden), **bf)
+        self.h2 = torch.empty((1, c.hidden), **bf)
+        self.act = torch.empty((1, c.intermediate), **bf)
+        self.down_out = torch.empty((1, c.hidden), **bf)
+        self.logits = torch.empty((1, c.vocab), **bf)
+        self.partial_o = torch.empty((1, self.num_splits, c.n_q, c.head_dim), dtype=torch.float32,
+                                     device=dev)
+        self.partial_lse = torch.empty((1, self.num_splits, c.n_q), dtype=torch.float32, device=dev)
+        self.graph: torch.cuda.CUDAGraph | None = None
+
+    # ------------------------------------------------------------------ step
+    def layer_run(self, i: int) -> None:
+        """One decoder layer on (self.h, self.x): leaves the next layer's
+        normalised input in self.h and the residual stream in self.x."""
+        c, L, st = self.cfg, self.layers[i], self.state
+        ops = torch_ops
+        ops.q4_0_gemv(self.h, L.qkv.qweight, c.qkv_rows, c.hidden, out=self.qkv_out)
+        ops.qknorm_rope_kv_write(self.qkv_out, L.q_norm, L.k_norm, self.cos_sin, st.positions,
+                                 st.slot_mapping, L.kv_cache[0], L.kv_cache[1], c.n_q, c.n_kv,
+                                 c.eps, q_out=self.q)
+        ops.splitkv_decode_merged(self.q, L.kv_cache[0], L.kv_cache[1], st.block_table,
+                                  st.seq_lens, self.num_splits, self.scale, self.partial_o,
+                                  self.partial_lse, out=self.attn)
+        ops.q4_0_gemv(self.attn, L.o_proj.qweight, c.hidden, c.n_q * c.head_dim, out=self.o)
+        ops.add_rmsnorm(self.o, self.x, L.post_norm, c.eps, out=self.h2, residual_out=self.x)
+        ops.q4_0_gemv_swiglu(self.h2, L.gate_up.qweight, c.intermediate, c.hidden, out=self.act)
+        ops.q4_0_gemv(self.act, L.down.qweight, c.hidden, c.intermediate, out=self.down_out)
+        nxt = self.layers[i + 1].input_norm if i + 1 < len(self.layers) else self.final_norm
+        ops.add_rmsnorm(self.down_out, self.x, nxt, c.eps, out=self.h, residual_out=self.x)
+
+    def enqueue_step(self) -> None:
+        c, st = self.cfg, self.state
+        ops = torch_ops
+        self.head.embed(st.ids, out=self.x)
+        ops.add_rmsnorm(self.x, None, self.layers[0].input_norm, c.eps, out=self.h)
+        for i in range(len(self.layers)):
+            self.layer_run(i)
+        ops.q4_0_gemv(self.h, self.head.q4_0_head, c.vocab, c.hidden, out=self.logits)
+        ops.argmax(self.logits, out=st.next_ids)
+        ops.decode_advance(st.next_ids, st.ids, st.positions, st.seq_lens, st.slot_mapping,
+                           st.block_table, c.block_size, tokens_out=st.tokens,
+                           forced_ids=st.forced, forced_len=st.forced_len)
+
+    def capture(self) -> None:
+        """Capture one decode step as a graph.  Clobbers the decode state;
+        call reset() afterwards."""
+        side = torch.cuda.Stream(device=self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(side):
+            self.enqueue_step()  # warm-up outside the graph
+        torch.cuda.current_stream(self.device).wait_stream(side)
+        torch.cuda.synchronize(self.device)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self.enqueue_step()
+        self.graph = g
+
+    def step(self) -> None:
+        if self.graph is not None:
+            self.graph.replay()
+        else:
+            self.enqueue_step()
+
+    # --------------------------------------------------------------- control
+    def reset(self, prompt: torch.Tensor) -> None:
+        """Position 0 holds prompt[0]; the advance kernel feeds the remaining
+        prompt tokens, then the model's own argmax."""
+        st = self.state
+        seq = prompt.to(device=self.device, dtype=torch.int64).view(-1)
+        if not 1 <= seq.numel() <= self.max_len:
+            raise ValueError("prompt must have 1..max_len tokens")
+        st.forced.zero_()
+        st.forced[0, :seq.numel()] = seq
+        st.forced_len.fill_(seq.numel())
+        st.tokens.fill_(-1)
+        st.tokens[0, 0] = seq[0]
+        st.ids.copy_(seq[:1])
+        st.positions.zero_()
+        st.seq_lens.fill_(1)
+        st.slot_mapping.copy_(st.block_table[0, :1].to(torch.int64) * self.cfg.block_size)
+
+    def generate(self, prompt: torch.Tensor, new_tokens: int) -> torch.Tensor:
+        """Greedy decode: feeds the prompt, then new_tokens generated tokens.
+        Returns the token ids by position (prompt followed by generated)."""
+        n = prompt.numel()
+        total = n + new_tokens
+        if total > self.max_len:
+            raise ValueError("prompt + new_tokens exceeds max_len")
+        self.reset(prompt)
+        for _ in range(total - 1):
+            self.step()
+        torch.cuda.synchronize(self.device)
+        return self.state.tokens[0, :total].clone()

@@ -33,6 +33,8 @@ SIGNATURES = {
     "smx_q4_0_gemv_swiglu": [_P, _P, _P, _P, _I64, _I64],
     "smx_splitkv_decode": [_P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32,
                            _I32, _I32, _F32],
+    "smx_splitkv_decode_merged": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32,
+                                  _I32, _I32, _I32, _I32, _F32],
     "smx_lse_merge": [_P, _P, _P, _P, _I32, _I32, _I32, _I32],
     "smx_add_rmsnorm": [_P, _P, _P, _P, _P, _P, _I64, _I64, _F32],
     "smx_qknorm_rope_kv_write": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32,
@@ -40,7 +42,8 @@ SIGNATURES = {
     "smx_silu_mul": [_P, _P, _P, _I64, _I64],
     "smx_embedding": [_P, _P, _P, _P, _I64, _I64, _I64],
     "smx_argmax_bf16": [_P, _P, _I64, _I64, _P],
-    "smx_decode_advance": [_P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32],
+    "smx_reshape_and_cache": [_P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32],
+    "smx_decode_advance": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32],
 }
 
 _lib = None

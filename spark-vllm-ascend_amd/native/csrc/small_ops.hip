@@ -205,15 +205,19 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const uint16_t* __restrict
   }
 }
 
-__global__ void decode_advance_kernel(const int64_t* __restrict__ next_ids, int64_t* ids,
-                                      int64_t* positions, int32_t* seq_lens,
+__global__ void decode_advance_kernel(const int64_t* __restrict__ next_ids,
+                                      const int64_t* __restrict__ forced_ids,
+                                      const int32_t* __restrict__ forced_len,
+                                      int64_t* ids, int64_t* positions, int32_t* seq_lens,
                                       int64_t* slot_mapping, const int32_t* block_table,
                                       int64_t* tokens_out, int rows, int max_blocks,
                                       int block_size, int max_len) {
   const int r = blockIdx.x * blockDim.x + threadIdx.x;
   if (r >= rows) return;
-  const int64_t nid = next_ids[r];
   const int64_t p = positions[r] + 1;
+  const int64_t nid = (forced_ids && p < forced_len[r] && p < max_len)
+                          ? forced_ids[(int64_t)r * max_len + p]
+                          : next_ids[r];
   ids[r] = nid;
   positions[r] = p;
   seq_lens[r] = (int32_t)(p + 1);
@@ -223,6 +227,22 @@ __global__ void decode_advance_kernel(const int64_t* __restrict__ next_ids, int6
                              p % block_size
                        : -1;
   if (tokens_out && p < max_len) tokens_out[(int64_t)r * max_len + p] = nid;
+}
+
+// One wave per (kv head, token): copies head_dim bf16 of K and of V.
+__global__ __launch_bounds__(64) void reshape_and_cache_kernel(
+    const uint16_t* __restrict__ key, const uint16_t* __restrict__ value,
+    uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache,
+    const int64_t* __restrict__ slot_mapping, int n_kv, int head_dim, int64_t cache_slots) {
+  const int h = blockIdx.x, t = blockIdx.y;
+  const int64_t slot = slot_mapping[t];
+  if (slot < 0 || slot >= cache_slots) return;
+  const int64_t src = ((int64_t)t * n_kv + h) * head_dim;
+  const int64_t dst = (slot * n_kv + h) * head_dim;
+  for (int i = threadIdx.x; i < head_dim; i += 64) {
+    k_cache[dst + i] = key[src + i];
+    v_cache[dst + i] = value[src + i];
+  }
 }
 
 }  // namespace
@@ -308,15 +328,36 @@ extern "C" int smx_argmax_bf16(void* stream, const void* logits, int64_t rows, i
   return (int)hipGetLastError();
 }
 
-extern "C" int smx_decode_advance(void* stream, const int64_t* next_ids, int64_t* ids,
+extern "C" int smx_reshape_and_cache(void* stream, const void* key, const void* value,
+                                     void* k_cache, void* v_cache, const int64_t* slot_mapping,
+                                     int32_t num_tokens, int32_t n_kv, int32_t head_dim,
+                                     int32_t num_blocks, int32_t block_size) {
+  SMX_REQUIRE(key && value && k_cache && v_cache && slot_mapping, "null pointer argument");
+  SMX_REQUIRE(num_tokens >= 1 && num_tokens <= 65535, "num_tokens must be in [1, 65535]");
+  SMX_REQUIRE(n_kv >= 1 && n_kv <= 65535 && head_dim >= 1 && head_dim <= 4096, "bad head shape");
+  SMX_REQUIRE(num_blocks >= 1 && block_size >= 1, "num_blocks and block_size must be >= 1");
+  SMX_REQUIRE((uintptr_t)slot_mapping % 8 == 0, "slot_mapping must be 8-byte aligned");
+  hipLaunchKernelGGL(smx::reshape_and_cache_kernel, dim3(n_kv, num_tokens), dim3(64), 0,
+                     (hipStream_t)stream, (const uint16_t*)key, (const uint16_t*)value,
+                     (uint16_t*)k_cache, (uint16_t*)v_cache, slot_mapping, n_kv, head_dim,
+                     (int64_t)num_blocks * block_size);
+  return (int)hipGetLastError();
+}
+
+extern "C" int smx_decode_advance(void* stream, const int64_t* next_ids,
+                                  const int64_t* forced_ids, const int32_t* forced_len, int64_t* ids,
                                   int64_t* positions, int32_t* seq_lens, int64_t* slot_mapping,
                                   const int32_t* block_table, int64_t* tokens_out, int32_t rows,
                                   int32_t max_blocks, int32_t block_size, int32_t max_len) {
   SMX_REQUIRE(next_ids && ids && positions && seq_lens && slot_mapping && block_table,
               "null pointer argument");
   SMX_REQUIRE(rows >= 1 && max_blocks >= 1 && block_size >= 1 && max_len >= 0, "bad sizes");
+  SMX_REQUIRE((forced_ids == nullptr) == (forced_len == nullptr),
+              "forced_ids and forced_len go together");
+  SMX_REQUIRE(!forced_ids || max_len >= 1, "forced_ids needs max_len >= 1");
   hipLaunchKernelGGL(smx::decode_advance_kernel, dim3((rows + 63) / 64), dim3(64), 0,
-                     (hipStream_t)stream, next_ids, ids, positions, seq_lens, slot_mapping,
-                     block_table, tokens_out, rows, max_blocks, block_size, max_len);
+                     (hipStream_t)stream, next_ids, forced_ids, forced_len, ids, positions,
+                     seq_lens, slot_mapping, block_table, tokens_out, rows, max_blocks,
+                     block_size, max_len);
   return (int)hipGetLastError();
 }

@@ -9,18 +9,12 @@
 // reported with lse = max + log(sum).
 //
 // Work decomposition (decode is HBM-bound: 512 bytes of K+V per token and kv
-// head against ~2k flops):
-//  * one workgroup (4 or 8 waves) per (split, kv head, sequence); the
-//    split's tokens are cut into contiguous 32-aligned chunks, one per wave;
-//  * a wave walks its chunk in 32-token tiles, pipelined in place: the next
-//    tile's K and V loads are in flight while the current tile is computed;
-//  * QK: 4 lanes per token, each owning 32 of the 128 dims for all 4 GQA
-//    heads (q lives in registers as bf16 pairs); v_dot2c_f32_bf16 + a quad
-//    reduction give the 4 scores;
-//  * PV: 16 lanes per token, each owning 8 dims; two tokens' V values are
-//    spliced into bf16 pairs with v_perm_b32 and meet the matching pair of
-//    bf16 probabilities (staged through LDS) in v_dot2c_f32_bf16;
-//  * the 4 waves' (max, sum, O) states are combined through LDS.
+// head against ~2k flops): one workgroup per (split, kv head, sequence) whose
+// waves stream 64-token blocks with all loads of a block in flight at once
+// (details at splitkv_decode_kernel), then a separate merge kernel.  The
+// merge is a second launch rather than a "last workgroup merges" epilogue:
+// on this multi-XCD part the device-scope fence that epilogue needs writes
+// back and invalidates each XCD's L2, which cost more than a launch.
 #include <math.h>
 
 #include "smx_common.h"
@@ -37,14 +31,6 @@ __device__ __forceinline__ float dppf(float v) { return dpp_f32<CTRL>(v); }
 constexpr int DPP_ROW_ROR4 = 0x124;
 constexpr int DPP_ROW_ROR8 = 0x128;
 
-// max over the 16 lane quads of a wave (values replicated inside a quad)
-__device__ __forceinline__ float quad_max_wave(float v) {
-  v = fmaxf(v, dppf<DPP_ROW_ROR4>(v));
-  v = fmaxf(v, dppf<DPP_ROW_ROR8>(v));
-  v = fmaxf(v, shfl_xor_f32(v, 16));
-  v = fmaxf(v, shfl_xor_f32(v, 32));
-  return v;
-}
 // sum over the 16 lanes of a wave that share lane & 3
 __device__ __forceinline__ float sum_stride4(float v) {
   v += dppf<DPP_ROW_ROR4>(v);
@@ -54,11 +40,30 @@ __device__ __forceinline__ float sum_stride4(float v) {
   return v;
 }
 
-// WAVES waves per workgroup; the split's tokens are cut into WAVES
-// contiguous 32-aligned chunks.  Within a wave, tiles are software-pipelined
-// in place: the next tile's K loads are issued as soon as the current K has
-// been consumed by QK, and its V loads as soon as PV has consumed V, so one
-// tile of registers keeps a load in flight during all arithmetic.
+// Max over the 16 lanes of a wave that share lane & 3.
+__device__ __forceinline__ float max_stride4(float v) {
+  v = fmaxf(v, dppf<DPP_ROW_ROR4>(v));
+  v = fmaxf(v, dppf<DPP_ROW_ROR8>(v));
+  v = fmaxf(v, shfl_xor_f32(v, 16));
+  v = fmaxf(v, shfl_xor_f32(v, 32));
+  return v;
+}
+
+constexpr int BLK = 64;  // tokens per wave block: all K and V loads of a block are issued at once
+
+// One workgroup of WAVES waves per (split, kv head, sequence).  Split s
+// covers [s*T, s*T + T) of the block table's capacity C (T = 32-aligned
+// ceil(C / num_splits)), clipped to the sequence length; its WAVES waves
+// take contiguous 32-aligned chunks and walk them in 64-token blocks.  Per block every K and V load is issued before
+// any arithmetic (128 VGPRs of data in flight per lane).
+//  QK: 8 lanes per token; lane c of a token owns the 16-byte chunks c and
+//      c + 8 of the 256-byte row, so each load instruction reads whole
+//      128-byte lines.  q (4 heads) is staged once per workgroup in LDS.
+//  softmax: after the 8-lane reduction every lane keeps the score of head
+//      lane & 3 only; maxima are reduced over the lanes sharing lane & 3.
+//  PV: 16 lanes per token, 8 dims each; two tokens' V are spliced into bf16
+//      pairs (v_perm_b32) that meet the bf16 probability pairs, staged in
+//      LDS, in v_dot2c_f32_bf16.
 template <int WAVES>
 __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
@@ -67,18 +72,30 @@ __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(
     float* __restrict__ part_lse, int num_splits, int max_blocks, int num_blocks, int bs_log2,
     int n_q, int n_kv, float scale_log2) {
   constexpr int NT = 64 * WAVES;
-  __shared__ uint32_t p2[WAVES][64];        // per wave: [jp][vt][h] bf16 probability pairs
-  __shared__ float o_w[WAVES][G * HD];       // per wave O (unnormalised)
+  __shared__ __attribute__((aligned(16))) uint32_t q_lds[G * HD / 2];  // 4 heads, bf16 pairs
+  __shared__ __attribute__((aligned(16))) uint32_t p2[WAVES][128];     // [jp 8][vt 4][h 4]
+  __shared__ float o_w[WAVES][G * HD];
   __shared__ float m_w[WAVES][G], l_w[WAVES][G];
   __shared__ int bad_w[WAVES];
 
   const int split = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  // A length beyond the block table is clamped to what the table can address.
-  const int L = min(seq_lens[seq], max_blocks << bs_log2);
-  const int tps = ((L + num_splits - 1) / num_splits + TILE - 1) / TILE * TILE;
+  // Split and wave boundaries follow from the block table's capacity, not
+  // from the sequence length, so the first page lookups, the length and q
+  // are all loaded in one round trip.
+  const int cap = max_blocks << bs_log2;
+  const int tps = ((cap + num_splits - 1) / num_splits + TILE - 1) / TILE * TILE;
+  const int wlen = ((tps + WAVES - 1) / WAVES + TILE - 1) / TILE * TILE;
   const int s0 = split * tps;
+  const int w0 = min(s0 + wave * wlen, cap);
+  const int32_t* bt = block_table + (int64_t)seq * max_blocks;
+  const int bt0 = bt[w0 < cap ? (w0 >> bs_log2) : 0];
+  const int bt1 = bt[w0 + 32 < cap ? ((w0 + 32) >> bs_log2) : 0];
+  const int L = min(seq_lens[seq], cap);
+  if (tid < G * HD / 8)
+    reinterpret_cast<u32x4*>(q_lds)[tid] =
+        reinterpret_cast<const u32x4*>(q + ((int64_t)seq * n_q + kvh * G) * HD)[tid];
   const int s1 = min(L, s0 + tps);
   float* po = part_o + (((int64_t)seq * num_splits + split) * n_q + kvh * G) * HD;
   float* pl = part_lse + ((int64_t)seq * num_splits + split) * n_q + kvh * G;
@@ -87,129 +104,113 @@ __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(
     if (tid < G) pl[tid] = -INFINITY;
     return;
   }
-  const int len = s1 - s0;
-  const int wlen = ((len + WAVES - 1) / WAVES + TILE - 1) / TILE * TILE;
-  const int w0 = s0 + wave * wlen;
   const int w1 = min(s1, w0 + wlen);
 
   const int bs = 1 << bs_log2;
   const int64_t tok_stride = (int64_t)n_kv * HD;
   const int64_t page_stride = tok_stride << bs_log2;
-  const int32_t* bt = block_table + (int64_t)seq * max_blocks;
 
-  // lane roles
-  const int qd = lane >> 2, dq = lane & 3;   // QK: token slot, 32-dim slice
+  const int tok = lane >> 3, dq = lane & 7;  // QK: token slot, 16-byte chunks dq, dq + 8
+  const int hsel = lane & 3;                 // softmax: the head this lane keeps
   const int vt = lane >> 4, dv = lane & 15;  // PV: token slot, 8-dim slice
 
-  // q for the 4 heads of this group, dims 32*dq .. 32*dq+31
-  u32x4 qr[G][4];
-  {
-    const uint16_t* qb = q + ((int64_t)seq * n_q + kvh * G) * HD + 32 * dq;
+  __syncthreads();
+  u32x4 qr[G][2];
 #pragma unroll
-    for (int h = 0; h < G; ++h)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) qr[h][i] = *reinterpret_cast<const u32x4*>(qb + h * HD + 8 * i);
+  for (int h = 0; h < G; ++h) {
+    qr[h][0] = reinterpret_cast<const u32x4*>(q_lds)[h * 16 + dq];
+    qr[h][1] = reinterpret_cast<const u32x4*>(q_lds)[h * 16 + dq + 8];
   }
 
   // A block-table entry outside [0, num_blocks) is never dereferenced: the
   // page is replaced by page 0 and the partial is poisoned with NaN below.
   bool bad_page = false;
-  auto page_of = [&](int t0) -> int64_t {
-    int pg = bt[t0 >> bs_log2];
+  auto half_base = [&](int t, int pg) -> int64_t {  // first token of a 32-token half
     if ((unsigned)pg >= (unsigned)num_blocks) {
       bad_page = true;
       pg = 0;
     }
-    return (int64_t)pg * page_stride + (int64_t)(t0 & (bs - 1)) * tok_stride + kvh * HD;
-  };
-  u32x4 kr[2][4];  // QK rounds 0/1: dims 32*dq .. 32*dq+31 of token t0 + 16*rr + qd
-  u32x4 vr[4][2];  // PV pairs jp: tokens t0 + 8jp + vt (+4), dims 8*dv .. 8*dv+7
-  // Tokens past the chunk end are loaded from the tile's first token (always
-  // valid) instead of branching; their scores are masked to -inf, so their
-  // probabilities are exactly 0.
-  auto load_k = [&](int t0, int64_t base) {
-#pragma unroll
-    for (int rr = 0; rr < 2; ++rr) {
-      const int t = rr * 16 + qd;
-      const int te = t0 + t < w1 ? t : 0;
-      const uint16_t* p = kc + base + te * tok_stride + 32 * dq;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) kr[rr][i] = *reinterpret_cast<const u32x4*>(p + 8 * i);
-    }
-  };
-  auto load_v = [&](int t0, int64_t base) {
-#pragma unroll
-    for (int jp = 0; jp < 4; ++jp)
-#pragma unroll
-      for (int hf = 0; hf < 2; ++hf) {
-        const int t = 8 * jp + vt + 4 * hf;
-        const int te = t0 + t < w1 ? t : 0;
-        vr[jp][hf] = *reinterpret_cast<const u32x4*>(vc + base + te * tok_stride + 8 * dv);
-      }
+    return (int64_t)pg * page_stride + (int64_t)(t & (bs - 1)) * tok_stride + kvh * HD;
   };
 
-  float m[G];
+  float m_mine = -INFINITY;  // running max (log2 domain) of head hsel
+  float l_lane = 0.f;        // running sum of head hsel over this lane's tokens
   float o[G][8];
 #pragma unroll
-  for (int h = 0; h < G; ++h) {
-    m[h] = -INFINITY;
+  for (int h = 0; h < G; ++h)
 #pragma unroll
     for (int i = 0; i < 8; ++i) o[h][i] = 0.f;
-  }
-  float l_lane = 0.f;  // running sum for head dq over this lane's tokens
 
-  if (w0 < w1) {
-    const int64_t b0 = page_of(w0);
-    load_k(w0, b0);
-    load_v(w0, b0);
-  }
-  for (int t0 = w0; t0 < w1; t0 += TILE) {
-    const bool more = t0 + TILE < w1;
-    const int64_t bnext = more ? page_of(t0 + TILE) : 0;
-
-    // ---- scores for the two QK rounds (tokens t0 + 16*rr + qd)
-    float s[2][G];
+  for (int t0 = w0; t0 < w1; t0 += BLK) {
+    const int64_t b0 = half_base(t0, t0 == w0 ? bt0 : bt[t0 >> bs_log2]);
+    const int64_t b1 = t0 + 32 < w1
+                           ? half_base(t0 + 32, t0 == w0 ? bt1 : bt[(t0 + 32) >> bs_log2])
+                           : b0;
+    // Tokens past the chunk end are loaded from the block's first token
+    // (always valid) instead of branching; their scores are masked to -inf.
+    auto tok_off = [&](int t) -> int64_t {
+      const int te = t0 + t < w1 ? t : 0;
+      return (te < 32 ? b0 : b1) + (int64_t)(te & 31) * tok_stride;
+    };
+    u32x4 kr[8][2];
 #pragma unroll
-    for (int rr = 0; rr < 2; ++rr) {
+    for (int r = 0; r < 8; ++r) {
+      const uint16_t* p = kc + tok_off(8 * r + tok);
+      kr[r][0] = reinterpret_cast<const u32x4*>(p)[dq];
+      kr[r][1] = reinterpret_cast<const u32x4*>(p)[dq + 8];
+    }
+    u32x4 vr[8][2];
+#pragma unroll
+    for (int jp = 0; jp < 8; ++jp)
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+        vr[jp][hf] = reinterpret_cast<const u32x4*>(vc + tok_off(8 * jp + vt + 4 * hf))[dv];
+
+    // ---- scores: token 8r + tok, head hsel
+    float sm[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      float a[G];
 #pragma unroll
       for (int h = 0; h < G; ++h) {
-        float a = 0.f;
+        float x = 0.f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          a = dot2_bf16(qr[h][i].x, kr[rr][i].x, a);
-          a = dot2_bf16(qr[h][i].y, kr[rr][i].y, a);
-          a = dot2_bf16(qr[h][i].z, kr[rr][i].z, a);
-          a = dot2_bf16(qr[h][i].w, kr[rr][i].w, a);
+        for (int c = 0; c < 2; ++c) {
+          x = dot2_bf16(qr[h][c].x, kr[r][c].x, x);
+          x = dot2_bf16(qr[h][c].y, kr[r][c].y, x);
+          x = dot2_bf16(qr[h][c].z, kr[r][c].z, x);
+          x = dot2_bf16(qr[h][c].w, kr[r][c].w, x);
         }
-        a = sum4(a) * scale_log2;
-        s[rr][h] = (t0 + rr * 16 + qd < w1) ? a : -INFINITY;
+        a[h] = sum8(x);
+      }
+      const float sv = hsel == 0 ? a[0] : hsel == 1 ? a[1] : hsel == 2 ? a[2] : a[3];
+      sm[r] = (t0 + 8 * r + tok < w1) ? sv * scale_log2 : -INFINITY;
+    }
+    // ---- online softmax (log2 domain) for head hsel
+    float mx = sm[0];
+#pragma unroll
+    for (int r = 1; r < 8; ++r) mx = fmaxf(mx, sm[r]);
+    mx = max_stride4(mx);
+    const float mn = fmaxf(m_mine, mx);
+    const float alpha = exp2f(m_mine - mn);
+    m_mine = mn;
+    const bool writer = (lane & 4) == 0;  // lanes dq and dq + 4 hold the same head
+    float psum = 0.f;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const float p = exp2f(sm[r] - mn);
+      psum += p;
+      if (writer) {
+        uint16_t* dst = reinterpret_cast<uint16_t*>(&p2[wave][(r * 4 + (tok & 3)) * 4 + hsel]);
+        dst[tok >> 2] = f32_to_bf16(p);
       }
     }
-    if (more) load_k(t0 + TILE, bnext);
-
-    // ---- online softmax update (log2 domain)
-    float alpha[G];
+    l_lane = l_lane * alpha + (writer ? psum : 0.f);
+    float alpha_h[G];
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
-      const float tmax = quad_max_wave(fmaxf(s[0][h], s[1][h]));
-      const float mn = fmaxf(m[h], tmax);
-      alpha[h] = exp2f(m[h] - mn);
-      m[h] = mn;
-    }
-    const float my_m = dq == 0 ? m[0] : dq == 1 ? m[1] : dq == 2 ? m[2] : m[3];
-    const float my_alpha = dq == 0 ? alpha[0] : dq == 1 ? alpha[1] : dq == 2 ? alpha[2] : alpha[3];
-    float p_sum = 0.f;
-#pragma unroll
-    for (int rr = 0; rr < 2; ++rr) {
-      const float sv = dq == 0 ? s[rr][0] : dq == 1 ? s[rr][1] : dq == 2 ? s[rr][2] : s[rr][3];
-      const float p = exp2f(sv - my_m);
-      p_sum += p;
-      const int t = rr * 16 + qd;  // tile-relative token
-      const int jp = t >> 3, within = t & 7;
-      uint16_t* dst = reinterpret_cast<uint16_t*>(&p2[wave][(jp * 4 + (within & 3)) * 4 + dq]);
-      dst[within >> 2] = f32_to_bf16(p);
-    }
-    l_lane = l_lane * my_alpha + p_sum;
+    for (int h = 0; h < G; ++h)
+      alpha_h[h] = __builtin_bit_cast(float,
+                                      __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), h));
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -218,9 +219,9 @@ __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(
 #pragma unroll
     for (int h = 0; h < G; ++h)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) o[h][i] *= alpha[h];
+      for (int i = 0; i < 8; ++i) o[h][i] *= alpha_h[h];
 #pragma unroll
-    for (int jp = 0; jp < 4; ++jp) {
+    for (int jp = 0; jp < 8; ++jp) {
       const u32x4 pp = *reinterpret_cast<const u32x4*>(&p2[wave][(jp * 4 + vt) * 4]);
       const u32x4 va = vr[jp][0], vb2 = vr[jp][1];
       uint32_t vpair[8];  // (v[t1][d], v[t2][d]) for the 8 dims
@@ -238,7 +239,6 @@ __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(
 #pragma unroll
         for (int i = 0; i < 8; ++i) o[h][i] = dot2_bf16(ph[h], vpair[i], o[h][i]);
     }
-    if (more) load_v(t0 + TILE, bnext);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -264,7 +264,7 @@ __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(
   if (lane == 0) bad_w[wave] = bad_page ? 1 : 0;
   if (lane < G) {
     l_w[wave][lane] = l_tot;
-    m_w[wave][lane] = lane == 0 ? m[0] : lane == 1 ? m[1] : lane == 2 ? m[2] : m[3];
+    m_w[wave][lane] = m_mine;  // lane h keeps head h
   }
   __syncthreads();
 
@@ -289,29 +289,69 @@ __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(
   }
 }
 
-// One workgroup per (q head, sequence); one thread per head dim.
-__global__ __launch_bounds__(128) void lse_merge_kernel(const float* __restrict__ part_o,
+// Log-sum-exp merge: one workgroup of 256 threads per (q head, sequence);
+// thread (half, d) folds the splits of its half with an online max, so every
+// load it needs (its partial values and the lse values, up to MB of each)
+// is issued at once; the two halves meet in LDS.
+__global__ __launch_bounds__(256) void lse_merge_kernel(const float* __restrict__ part_o,
                                                         const float* __restrict__ part_lse,
                                                         uint16_t* __restrict__ out,
-                                                        int num_splits, int n_q, int hd) {
+                                                        int num_splits, int n_q) {
+  constexpr int MB = 32;
+  __shared__ float xm[HD], xl[HD], xa[HD];
   const int h = blockIdx.x, seq = blockIdx.y;
+  const int d = threadIdx.x & (HD - 1), half = threadIdx.x >> 7;
+  const int per = (num_splits + 1) / 2;
+  const int sb = half * per, se = min(num_splits, sb + per);
   const float* lse = part_lse + (int64_t)seq * num_splits * n_q + h;
-  float mx = -INFINITY;
-  for (int s = 0; s < num_splits; ++s) mx = fmaxf(mx, lse[(int64_t)s * n_q]);
-  float den = 0.f;
-  for (int s = 0; s < num_splits; ++s) {
-    const float v = lse[(int64_t)s * n_q];
-    den += v == -INFINITY ? 0.f : expf(v - mx);
-  }
-  for (int d = threadIdx.x; d < hd; d += blockDim.x) {
-    float acc = 0.f;
-    for (int s = 0; s < num_splits; ++s) {
-      const float v = lse[(int64_t)s * n_q];
-      if (v == -INFINITY) continue;
-      const float wgt = expf(v - mx) / den;
-      acc += part_o[(((int64_t)seq * num_splits + s) * n_q + h) * hd + d] * wgt;
+  const int64_t stride = (int64_t)n_q * HD;
+  const float* src = part_o + ((int64_t)seq * num_splits * n_q + h) * HD + d;
+  float m = -INFINITY, l = 0.f, acc = 0.f;
+  bool poisoned = false;  // a NaN partial (e.g. a bad block-table entry) poisons the output
+  for (int b0 = sb; b0 < se; b0 += MB) {
+    float lv[MB], pv[MB];
+#pragma unroll
+    for (int j = 0; j < MB; ++j) {
+      const bool ok = b0 + j < se;
+      lv[j] = ok ? lse[(int64_t)(b0 + j) * n_q] : -INFINITY;
+      pv[j] = ok ? src[(b0 + j) * stride] : 0.f;
     }
-    out[((int64_t)seq * n_q + h) * hd + d] = f32_to_bf16(acc);
+    float mb = m;
+#pragma unroll
+    for (int j = 0; j < MB; ++j) {
+      poisoned |= lv[j] != lv[j];
+      mb = fmaxf(mb, lv[j]);
+    }
+    if (mb != -INFINITY) {
+      const float a = expf(m - mb);
+      l *= a;
+      acc *= a;
+#pragma unroll
+      for (int j = 0; j < MB; ++j) {
+        const float wj = lv[j] == -INFINITY ? 0.f : expf(lv[j] - mb);
+        l += wj;
+        acc += wj * pv[j];
+      }
+      m = mb;
+    }
+  }
+  if (poisoned) acc = __builtin_nanf("");
+  if (half == 1) {
+    xm[d] = m;
+    xl[d] = l;
+    xa[d] = acc;
+  }
+  __syncthreads();
+  if (half == 0) {
+    const float m2 = xm[d], l2 = xl[d], a2 = xa[d];
+    const float mt = fmaxf(m, m2);
+    const float f1 = m == -INFINITY ? 0.f : expf(m - mt);
+    const float f2 = m2 == -INFINITY ? 0.f : expf(m2 - mt);
+    const float lt = l * f1 + l2 * f2;
+    const float at = acc * f1 + a2 * f2;
+    const bool nan_in = acc != acc || a2 != a2;
+    out[((int64_t)seq * n_q + h) * HD + d] =
+        f32_to_bf16(nan_in ? __builtin_nanf("") : (lt > 0.f ? at / lt : 0.f));
   }
 }
 
@@ -320,44 +360,87 @@ __global__ __launch_bounds__(128) void lse_merge_kernel(const float* __restrict_
 
 #include "smx_abi_util.h"
 
+namespace {
+int launch_splitkv(void* stream, const void* q, const void* k_cache, const void* v_cache,
+                   const int32_t* block_table, const int32_t* seq_lens, float* partial_o,
+                   float* partial_lse, int32_t num_seqs, int32_t num_splits, int32_t max_blocks,
+                   int32_t num_blocks, int32_t block_size, int32_t n_q, int32_t n_kv,
+                   float scale) {
+  int bs_log2 = 0;
+  while ((1 << bs_log2) < block_size) ++bs_log2;
+  const float scale_log2 = scale * 1.44269504088896340736f;
+  // One 64-token block per wave: the wave count follows the split size.
+  const int64_t cap = (int64_t)max_blocks * block_size;
+  const int64_t tps = ((cap + num_splits - 1) / num_splits + 31) / 32 * 32;
+  int waves = tps <= 64 ? 1 : tps <= 128 ? 2 : tps <= 256 ? 4 : 8;
+  const char* e = getenv("SMX_ATTN_WAVES");  // override for tuning sweeps
+  if (e && (atoi(e) == 1 || atoi(e) == 2 || atoi(e) == 4 || atoi(e) == 8)) waves = atoi(e);
+  const dim3 grid(num_splits, n_kv, num_seqs);
+#define SMX_ATTN_LAUNCH(W)                                                                   \
+  hipLaunchKernelGGL(smx::splitkv_decode_kernel<W>, grid, dim3(64 * W), 0, (hipStream_t)stream, \
+                     (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache,  \
+                     block_table, seq_lens, partial_o, partial_lse, num_splits, max_blocks,   \
+                     num_blocks, bs_log2, n_q, n_kv, scale_log2)
+  if (waves == 8) SMX_ATTN_LAUNCH(8);
+  else if (waves == 4) SMX_ATTN_LAUNCH(4);
+  else if (waves == 2) SMX_ATTN_LAUNCH(2);
+  else SMX_ATTN_LAUNCH(1);
+#undef SMX_ATTN_LAUNCH
+  return (int)hipGetLastError();
+}
+
+int launch_merge(void* stream, const float* partial_o, const float* partial_lse, void* out,
+                 int32_t num_seqs, int32_t num_splits, int32_t n_q) {
+  hipLaunchKernelGGL(smx::lse_merge_kernel, dim3(n_q, num_seqs), dim3(256), 0,
+                     (hipStream_t)stream, partial_o, partial_lse, (uint16_t*)out, num_splits,
+                     n_q);
+  return (int)hipGetLastError();
+}
+}  // namespace
+
+#define SMX_SPLITKV_CHECKS()                                                                     \
+  SMX_REQUIRE(q && k_cache && v_cache && block_table && seq_lens && partial_o && partial_lse,    \
+              "null pointer argument");                                                          \
+  SMX_REQUIRE(num_seqs >= 1 && num_seqs <= 65535, "num_seqs must be in [1, 65535]");             \
+  SMX_REQUIRE(num_splits >= 1 && num_splits <= 4096, "num_splits must be in [1, 4096]");         \
+  SMX_REQUIRE(max_blocks >= 1 && num_blocks >= 1, "max_blocks and num_blocks must be >= 1");     \
+  SMX_REQUIRE(head_dim == 128, "head_dim must be 128");                                          \
+  SMX_REQUIRE(n_kv >= 1 && n_q == 4 * n_kv && n_kv <= 65535, "need n_q == 4 * n_kv (GQA 4:1)"); \
+  SMX_REQUIRE(block_size >= 32 && block_size <= 4096 && (block_size & (block_size - 1)) == 0,    \
+              "block_size must be a power of two in [32, 4096]");                                \
+  SMX_REQUIRE(scale > 0.f && isfinite(scale), "scale must be positive and finite");              \
+  SMX_REQUIRE((uintptr_t)q % 16 == 0 && (uintptr_t)k_cache % 16 == 0 &&                          \
+                  (uintptr_t)v_cache % 16 == 0 && (uintptr_t)block_table % 4 == 0 &&             \
+                  (uintptr_t)seq_lens % 4 == 0 && (uintptr_t)partial_o % 4 == 0 &&               \
+                  (uintptr_t)partial_lse % 4 == 0,                                               \
+              "q, k_cache and v_cache must be 16-byte aligned; int/float arrays 4-byte aligned")
+
 extern "C" int smx_splitkv_decode(void* stream, const void* q, const void* k_cache,
                                   const void* v_cache, const int32_t* block_table,
                                   const int32_t* seq_lens, float* partial_o, float* partial_lse,
                                   int32_t num_seqs, int32_t num_splits, int32_t max_blocks,
                                   int32_t num_blocks, int32_t block_size, int32_t n_q,
                                   int32_t n_kv, int32_t head_dim, float scale) {
-  SMX_REQUIRE(q && k_cache && v_cache && block_table && seq_lens && partial_o && partial_lse,
-              "null pointer argument");
-  SMX_REQUIRE(num_seqs >= 1 && num_seqs <= 65535, "num_seqs must be in [1, 65535]");
-  SMX_REQUIRE(num_splits >= 1 && num_splits <= 4096, "num_splits must be in [1, 4096]");
-  SMX_REQUIRE(max_blocks >= 1 && num_blocks >= 1, "max_blocks and num_blocks must be >= 1");
-  SMX_REQUIRE(head_dim == 128, "head_dim must be 128");
-  SMX_REQUIRE(n_kv >= 1 && n_q == 4 * n_kv && n_kv <= 65535, "need n_q == 4 * n_kv (GQA 4:1)");
-  SMX_REQUIRE(block_size >= 32 && block_size <= 4096 && (block_size & (block_size - 1)) == 0,
-              "block_size must be a power of two in [32, 4096]");
-  SMX_REQUIRE(scale > 0.f && isfinite(scale), "scale must be positive and finite");
-  SMX_REQUIRE((uintptr_t)q % 16 == 0 && (uintptr_t)k_cache % 16 == 0 &&
-                  (uintptr_t)v_cache % 16 == 0 && (uintptr_t)block_table % 4 == 0 &&
-                  (uintptr_t)seq_lens % 4 == 0 && (uintptr_t)partial_o % 4 == 0 &&
-                  (uintptr_t)partial_lse % 4 == 0,
-              "q, k_cache and v_cache must be 16-byte aligned; int/float arrays 4-byte aligned");
-  int bs_log2 = 0;
-  while ((1 << bs_log2) < block_size) ++bs_log2;
-  const float scale_log2 = scale * 1.44269504088896340736f;
-  int waves = 4;
-  const char* e = getenv("SMX_ATTN_WAVES");  // 4 or 8 waves per workgroup, for tuning sweeps
-  if (e && atoi(e) == 8) waves = 8;
-  if (waves == 8)
-    hipLaunchKernelGGL(smx::splitkv_decode_kernel<8>, dim3(num_splits, n_kv, num_seqs), dim3(512),
-                       0, (hipStream_t)stream, (const uint16_t*)q, (const uint16_t*)k_cache,
-                       (const uint16_t*)v_cache, block_table, seq_lens, partial_o, partial_lse,
-                       num_splits, max_blocks, num_blocks, bs_log2, n_q, n_kv, scale_log2);
-  else
-    hipLaunchKernelGGL(smx::splitkv_decode_kernel<4>, dim3(num_splits, n_kv, num_seqs), dim3(256),
-                       0, (hipStream_t)stream, (const uint16_t*)q, (const uint16_t*)k_cache,
-                       (const uint16_t*)v_cache, block_table, seq_lens, partial_o, partial_lse,
-                       num_splits, max_blocks, num_blocks, bs_log2, n_q, n_kv, scale_log2);
-  return (int)hipGetLastError();
+  SMX_SPLITKV_CHECKS();
+  return launch_splitkv(stream, q, k_cache, v_cache, block_table, seq_lens, partial_o,
+                        partial_lse, num_seqs, num_splits, max_blocks, num_blocks, block_size, n_q,
+                        n_kv, scale);
+}
+
+extern "C" int smx_splitkv_decode_merged(void* stream, const void* q, const void* k_cache,
+                                         const void* v_cache, const int32_t* block_table,
+                                         const int32_t* seq_lens, float* partial_o,
+                                         float* partial_lse, void* out, int32_t num_seqs,
+                                         int32_t num_splits, int32_t max_blocks,
+                                         int32_t num_blocks, int32_t block_size, int32_t n_q,
+                                         int32_t n_kv, int32_t head_dim, float scale) {
+  SMX_SPLITKV_CHECKS();
+  SMX_REQUIRE(out && (uintptr_t)out % 2 == 0, "out must be non-null and 2-byte aligned");
+  const int rc = launch_splitkv(stream, q, k_cache, v_cache, block_table, seq_lens, partial_o,
+                                partial_lse, num_seqs, num_splits, max_blocks, num_blocks,
+                                block_size, n_q, n_kv, scale);
+  if (rc) return rc;
+  return launch_merge(stream, partial_o, partial_lse, out, num_seqs, num_splits, n_q);
 }
 
 extern "C" int smx_lse_merge(void* stream, const float* partial_o, const float* partial_lse,
@@ -366,12 +449,9 @@ extern "C" int smx_lse_merge(void* stream, const float* partial_o, const float* 
   SMX_REQUIRE(partial_o && partial_lse && out, "null pointer argument");
   SMX_REQUIRE(num_seqs >= 1 && num_seqs <= 65535, "num_seqs must be in [1, 65535]");
   SMX_REQUIRE(num_splits >= 1 && num_splits <= 4096, "num_splits must be in [1, 4096]");
-  SMX_REQUIRE(n_q >= 1 && head_dim >= 1 && head_dim <= 1024, "bad n_q or head_dim");
+  SMX_REQUIRE(head_dim == 128 && n_q >= 1 && n_q <= 65535, "head_dim must be 128");
   SMX_REQUIRE((uintptr_t)out % 2 == 0 && (uintptr_t)partial_o % 4 == 0 &&
                   (uintptr_t)partial_lse % 4 == 0,
               "misaligned pointer");
-  hipLaunchKernelGGL(smx::lse_merge_kernel, dim3(n_q, num_seqs), dim3(128), 0,
-                     (hipStream_t)stream, partial_o, partial_lse, (uint16_t*)out, num_splits,
-                     n_q, head_dim);
-  return (int)hipGetLastError();
+  return launch_merge(stream, partial_o, partial_lse, out, num_seqs, num_splits, n_q);
 }

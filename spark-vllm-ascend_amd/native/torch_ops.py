@@ -105,6 +105,35 @@ def splitkv_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor
     return partial_o, partial_lse
 
 
+def splitkv_decode_merged(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                          block_table: torch.Tensor, seq_lens: torch.Tensor, num_splits: int,
+                          scale: float, partial_o: torch.Tensor, partial_lse: torch.Tensor,
+                          out: torch.Tensor | None = None) -> torch.Tensor:
+    """Split-KV decode then the LSE merge, enqueued by one call; partial_o /
+    partial_lse are the workspace between the two kernels."""
+    _need(q.dim() == 3 and k_cache.dim() == 4, "q must be [seqs, n_q, hd], caches 4-D")
+    num_seqs, n_q, hd = q.shape
+    num_blocks, bs, n_kv, hd2 = k_cache.shape
+    _need(hd == hd2, "head_dim mismatch between q and the cache")
+    _need(tuple(v_cache.shape) == tuple(k_cache.shape), "k_cache and v_cache shapes differ")
+    _check(q, "q", BF16)
+    _check(k_cache, "k_cache", BF16, device=q.device)
+    _check(v_cache, "v_cache", BF16, device=q.device)
+    _check(block_table, "block_table", torch.int32, device=q.device)
+    _need(block_table.dim() == 2 and block_table.shape[0] == num_seqs, "block_table must be [seqs, max_blocks]")
+    _check(seq_lens, "seq_lens", torch.int32, num_seqs, q.device)
+    _check(partial_o, "partial_o", torch.float32, num_seqs * num_splits * n_q * hd, q.device)
+    _check(partial_lse, "partial_lse", torch.float32, num_seqs * num_splits * n_q, q.device)
+    if out is None:
+        out = torch.empty((num_seqs, n_q, hd), dtype=BF16, device=q.device)
+    _check(out, "out", BF16, num_seqs * n_q * hd, q.device)
+    call("smx_splitkv_decode_merged", _stream(q), q.data_ptr(), k_cache.data_ptr(),
+         v_cache.data_ptr(), block_table.data_ptr(), seq_lens.data_ptr(), partial_o.data_ptr(),
+         partial_lse.data_ptr(), out.data_ptr(), num_seqs, num_splits,
+         block_table.shape[1], num_blocks, bs, n_q, n_kv, hd, float(scale))
+    return out
+
+
 def lse_merge(partial_o: torch.Tensor, partial_lse: torch.Tensor,
               out: torch.Tensor | None = None) -> torch.Tensor:
     _need(partial_o.dim() == 4, "partial_o must be [seqs, splits, n_q, hd]")
@@ -205,9 +234,29 @@ def argmax(logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tenso
     return out
 
 
+def reshape_and_cache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
+                      v_cache: torch.Tensor, slot_mapping: torch.Tensor) -> None:
+    """key, value: [num_tokens, n_kv, head_dim]; caches [blocks, bs, n_kv, head_dim]."""
+    num_blocks, bs, n_kv, hd = k_cache.shape
+    num_tokens = slot_mapping.numel()
+    _check(key, "key", BF16, num_tokens * n_kv * hd)
+    _check(value, "value", BF16, num_tokens * n_kv * hd, key.device)
+    _check(k_cache, "k_cache", BF16, device=key.device)
+    _check(v_cache, "v_cache", BF16, device=key.device)
+    _need(tuple(v_cache.shape) == tuple(k_cache.shape), "k_cache and v_cache shapes differ")
+    _check(slot_mapping, "slot_mapping", torch.int64, num_tokens, key.device)
+    call("smx_reshape_and_cache", _stream(key), key.data_ptr(), value.data_ptr(),
+         k_cache.data_ptr(), v_cache.data_ptr(), slot_mapping.data_ptr(), num_tokens, n_kv, hd,
+         num_blocks, bs)
+
+
 def decode_advance(next_ids: torch.Tensor, ids: torch.Tensor, positions: torch.Tensor,
                    seq_lens: torch.Tensor, slot_mapping: torch.Tensor, block_table: torch.Tensor,
-                   block_size: int, tokens_out: torch.Tensor | None = None) -> None:
+                   block_size: int, tokens_out: torch.Tensor | None = None,
+                   forced_ids: torch.Tensor | None = None,
+                   forced_len: torch.Tensor | None = None) -> None:
+    """forced_ids [rows, max_len] int64 with forced_len [rows] int32 on the
+    device; tokens_out [rows, max_len] int64 (same max_len)."""
     rows = ids.numel()
     _check(next_ids, "next_ids", torch.int64, rows)
     _check(ids, "ids", torch.int64, rows, next_ids.device)
@@ -216,12 +265,19 @@ def decode_advance(next_ids: torch.Tensor, ids: torch.Tensor, positions: torch.T
     _check(slot_mapping, "slot_mapping", torch.int64, rows, next_ids.device)
     _check(block_table, "block_table", torch.int32, device=next_ids.device)
     _need(block_table.dim() == 2 and block_table.shape[0] == rows, "block_table must be [rows, max_blocks]")
+    _need((forced_ids is None) == (forced_len is None), "forced_ids and forced_len go together")
     max_len = 0
-    if tokens_out is not None:
-        _check(tokens_out, "tokens_out", torch.int64, device=next_ids.device)
-        _need(tokens_out.dim() == 2 and tokens_out.shape[0] == rows, "tokens_out must be [rows, max_len]")
-        max_len = tokens_out.shape[1]
-    call("smx_decode_advance", _stream(ids), next_ids.data_ptr(), ids.data_ptr(),
+    for name, t in (("tokens_out", tokens_out), ("forced_ids", forced_ids)):
+        if t is not None:
+            _check(t, name, torch.int64, device=next_ids.device)
+            _need(t.dim() == 2 and t.shape[0] == rows, f"{name} must be [rows, max_len]")
+            _need(max_len in (0, t.shape[1]), "tokens_out and forced_ids need the same max_len")
+            max_len = t.shape[1]
+    if forced_len is not None:
+        _check(forced_len, "forced_len", torch.int32, rows, next_ids.device)
+    call("smx_decode_advance", _stream(ids), next_ids.data_ptr(),
+         forced_ids.data_ptr() if forced_ids is not None else None,
+         forced_len.data_ptr() if forced_len is not None else None, ids.data_ptr(),
          positions.data_ptr(), seq_lens.data_ptr(), slot_mapping.data_ptr(), block_table.data_ptr(),
          tokens_out.data_ptr() if tokens_out is not None else None, rows, block_table.shape[1],
          block_size, max_len)

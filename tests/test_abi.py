@@ -52,6 +52,9 @@ def test_bindings_cover_header():
     ("smx_splitkv_decode", (None, 16, 16, 16, 16, 16, 16, 16, 1, 0, 8, 8, 128, 32, 8, 128, 0.1)),
     ("smx_splitkv_decode", (None, 16, 16, 16, 16, 16, 16, 16, 1, 4, 8, 8, 128, 32, 8, 128, -1.0)),
     ("smx_lse_merge", (None, 16, 16, 16, 1, 0, 32, 128)),
+    ("smx_lse_merge", (None, 16, 16, 16, 1, 4, 32, 64)),
+    ("smx_splitkv_decode_merged", (None, 16, 16, 16, 16, 16, 16, 16, None, 1, 4, 8, 8, 128, 32, 8, 128, 0.1)),
+    ("smx_splitkv_decode_merged", (None, 16, 16, 16, 16, 16, 16, 16, 16, 1, 4, 8, 8, 100, 32, 8, 128, 0.1)),
     ("smx_add_rmsnorm", (None, 16, 16, 16, 16, 16, 1, 2561, 1e-6)),
     ("smx_add_rmsnorm", (None, 16, 16, 16, 16, 16, 1, 32768, 1e-6)),
     ("smx_add_rmsnorm", (None, 8, 16, 16, 16, 16, 1, 2560, 1e-6)),
@@ -59,7 +62,10 @@ def test_bindings_cover_header():
     ("smx_silu_mul", (None, 16, 16, 0, 10)),
     ("smx_embedding", (None, 16, 16, 16, 0, 10, 10)),
     ("smx_argmax_bf16", (None, 16, 0, 10, 16)),
-    ("smx_decode_advance", (None, 16, 16, 16, 16, 16, 16, None, 0, 1, 1, 0)),
+    ("smx_decode_advance", (None, 16, None, None, 16, 16, 16, 16, 16, None, 0, 1, 1, 0)),
+    ("smx_decode_advance", (None, 16, None, 16, 16, 16, 16, 16, 16, None, 1, 1, 1, 0)),
+    ("smx_decode_advance", (None, 16, 16, 16, 16, 16, 16, 16, 16, None, 1, 1, 1, 0)),
+    ("smx_reshape_and_cache", (None, 16, 16, 16, 16, 16, 0, 8, 128, 4, 128)),
 ])
 def test_invalid_arguments_rejected_on_host(call, args):
     native = pkg("native")

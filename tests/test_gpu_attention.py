@@ -44,25 +44,33 @@ def _case(rng, lengths, bs, extra_blocks=3):
     return q, kc, vc, table
 
 
-def _run(ops, dev, q, kc, vc, table, lengths, splits, scale):
+def _run(ops, dev, q, kc, vc, table, lengths, splits, scale, merged=False):
+    """Separate split-KV and LSE-merge calls, or the one-call merged entry."""
     import torch
-    po, pl = ops.splitkv_decode(bf16_dev(q, dev), bf16_dev(kc, dev), bf16_dev(vc, dev),
-                                torch.from_numpy(table).to(dev),
-                                torch.tensor(lengths, dtype=torch.int32, device=dev), splits, scale)
-    out = ops.lse_merge(po, pl)
+    args = (bf16_dev(q, dev), bf16_dev(kc, dev), bf16_dev(vc, dev), torch.from_numpy(table).to(dev),
+            torch.tensor(lengths, dtype=torch.int32, device=dev), splits, scale)
+    if merged:
+        nq = q.shape[1]
+        po = torch.empty((len(lengths), splits, nq, HD), dtype=torch.float32, device=dev)
+        pl = torch.empty((len(lengths), splits, nq), dtype=torch.float32, device=dev)
+        out = ops.splitkv_decode_merged(*args, po, pl)
+    else:
+        po, pl = ops.splitkv_decode(*args)
+        out = ops.lse_merge(po, pl)
     return f32_of(out), po.cpu().numpy(), pl.cpu().numpy()
 
 
+@pytest.mark.parametrize("merged", [False, True])
 @pytest.mark.parametrize("L", [1, 2, 31, 32, 33, 127, 128, 129, 300, 2048, 4096, 6144])
-@pytest.mark.parametrize("splits", [1, 4, 8, 16, 32])
-def test_splitkv_vs_fp64(ops, dev, L, splits):
+@pytest.mark.parametrize("splits", [1, 4, 8, 16, 32, 64])
+def test_splitkv_vs_fp64(ops, dev, L, splits, merged):
     if L > 2048 and splits in (1, 4) and L != 6144:
         pytest.skip("covered by other split counts")
     rng = np.random.default_rng(L * 31 + splits)
     bs = 128
     q, kc, vc, table = _case(rng, [L], bs)
     scale = HD ** -0.5
-    out, po, pl = _run(ops, dev, q, kc, vc, table, [L], splits, scale)
+    out, po, pl = _run(ops, dev, q, kc, vc, table, [L], splits, scale, merged=merged)
     qf, kf, vf = (bf16_bits_to_f32(a) for a in (q, kc, vc))
     k = oatt.gather_paged(kf, table[0], L)
     v = oatt.gather_paged(vf, table[0], L)
@@ -70,7 +78,7 @@ def test_splitkv_vs_fp64(ops, dev, L, splits):
     err = np.max(np.abs(out.reshape(N_Q, HD) - ref))
     assert err < 2e-2, f"merged output err {err}"
     # per-split partials against the oracle's online softmax
-    bounds = oatt.split_bounds(L, splits)
+    bounds = oatt.split_bounds(L, splits, table.shape[1] * bs)
     opo, opl = oatt.splitkv_partials(qf[0], k, v, scale, bounds)
     finite = np.isfinite(opl)
     np.testing.assert_array_equal(np.isfinite(pl[0]), finite)
@@ -92,13 +100,14 @@ def test_block_sizes(ops, dev, bs):
     assert np.max(np.abs(out.reshape(N_Q, HD) - ref)) < 2e-2
 
 
-def test_ragged_batch(ops, dev):
+@pytest.mark.parametrize("merged", [False, True])
+def test_ragged_batch(ops, dev, merged):
     rng = np.random.default_rng(5)
     lengths = [512, 3000, 77, 32768 // 4, 1]
     bs = 128
     q, kc, vc, table = _case(rng, lengths, bs)
     scale = HD ** -0.5
-    out, _, _ = _run(ops, dev, q, kc, vc, table, lengths, 16, scale)
+    out, _, _ = _run(ops, dev, q, kc, vc, table, lengths, 16, scale, merged=merged)
     qf, kf, vf = (bf16_bits_to_f32(a) for a in (q, kc, vc))
     out = out.reshape(len(lengths), N_Q, HD)
     for i, L in enumerate(lengths):
@@ -133,6 +142,16 @@ def test_equal_keys_give_mean_of_values(ops, dev):
     vf = oatt.gather_paged(bf16_bits_to_f32(vc), table[0], L)
     ref = np.repeat(vf.mean(axis=0), N_Q // N_KV, axis=0)
     assert np.max(np.abs(out.reshape(N_Q, HD) - ref)) < 1e-2
+
+
+def test_merged_equals_two_call_path_bitwise(ops, dev):
+    rng = np.random.default_rng(12)
+    L = 5000
+    q, kc, vc, table = _case(rng, [L], 128)
+    a, _, _ = _run(ops, dev, q, kc, vc, table, [L], 32, HD ** -0.5)
+    for _ in range(2):
+        b, _, _ = _run(ops, dev, q, kc, vc, table, [L], 32, HD ** -0.5, merged=True)
+        np.testing.assert_array_equal(a, b)
 
 
 def test_bad_block_table_entry_poisons_only(ops, dev):

@@ -1,0 +1,94 @@
+"""Pins for the oracle's split-KV attention (CPU only): invariants that any
+correct implementation satisfies, checked against the float64 textbook
+attention, which is itself checked on hand-computable cases."""
+import numpy as np
+import pytest
+
+from oracle import attention as oatt
+from oracle.bf16 import round_bf16
+
+
+def rand_case(rng, L, n_q=8, n_kv=2, hd=128):
+    q = round_bf16(rng.standard_normal((n_q, hd)).astype(np.float32))
+    k = round_bf16(rng.standard_normal((L, n_kv, hd)).astype(np.float32))
+    v = round_bf16(rng.standard_normal((L, n_kv, hd)).astype(np.float32))
+    return q, k, v
+
+
+def test_textbook_two_tokens_by_hand():
+    q = np.zeros((4, 2), np.float32)
+    q[:, 0] = 1.0
+    k = np.array([[[0.0, 0.0]], [[np.log(3.0), 0.0]]], np.float32)  # scores 0, log 3
+    v = np.array([[[1.0, 0.0]], [[0.0, 1.0]]], np.float32)
+    out = oatt.attention_f64(q, k, v, 1.0)
+    np.testing.assert_allclose(out[0], [0.25, 0.75], rtol=1e-7)
+
+
+def test_ctx_one_gives_v0():
+    rng = np.random.default_rng(0)
+    q, k, v = rand_case(rng, 1)
+    out = oatt.attention_f64(q, k, v, 0.1)
+    np.testing.assert_allclose(out, np.repeat(v[0], 4, axis=0), rtol=1e-12)
+    po, pl = oatt.splitkv_partials(q, k, v, 0.1, oatt.split_bounds(1, 4))
+    np.testing.assert_allclose(round_bf16(po[0]), np.repeat(v[0], 4, axis=0), rtol=1e-2)
+
+
+@pytest.mark.parametrize("L", [5, 31, 32, 33, 300, 1000])
+@pytest.mark.parametrize("S", [1, 2, 3, 4, 8, 16, 32])
+def test_split_count_invariance(L, S):
+    rng = np.random.default_rng(L * 100 + S)
+    q, k, v = rand_case(rng, L)
+    ref = oatt.attention_f64(q, k, v, 128 ** -0.5)
+    po, pl = oatt.splitkv_partials(q, k, v, 128 ** -0.5, oatt.split_bounds(L, S))
+    out = oatt.lse_merge(po, pl)
+    assert np.max(np.abs(out - ref)) < 1e-2
+
+
+def test_split_bounds_cover_exactly():
+    for L in (1, 31, 32, 33, 4096, 6144, 6145):
+        for S in (1, 3, 4, 32, 64):
+            for cap in (None, L + 100, 8192):
+                b = oatt.split_bounds(L, S, cap)
+                covered = [t for a, e in b for t in range(a, e)]
+                assert covered == list(range(L))
+                assert all(a % 32 == 0 for a, e in b if a < e)
+
+
+def test_equal_keys_mean_of_values():
+    rng = np.random.default_rng(2)
+    q, k, v = rand_case(rng, 200)
+    k[:] = k[0:1]
+    ref = np.repeat(v.mean(axis=0), 4, axis=0)
+    np.testing.assert_allclose(oatt.attention_f64(q, k, v, 0.2), ref, rtol=1e-6, atol=1e-6)
+    po, pl = oatt.splitkv_partials(q, k, v, 0.2, oatt.split_bounds(200, 3))
+    assert np.max(np.abs(oatt.lse_merge(po, pl) - ref)) < 1e-2
+
+
+def test_paging_and_permutation_invariance():
+    rng = np.random.default_rng(3)
+    L, bs, nblk = 300, 32, 12
+    kc = round_bf16(rng.standard_normal((nblk, bs, 2, 128)).astype(np.float32))
+    vc = round_bf16(rng.standard_normal((nblk, bs, 2, 128)).astype(np.float32))
+    q = round_bf16(rng.standard_normal((8, 128)).astype(np.float32))
+    table = rng.permutation(nblk)[:10]
+    a, _, _ = oatt.splitkv_decode(q, kc, vc, table, L, 4, 0.1)
+    perm = rng.permutation(nblk)
+    inv = np.argsort(perm)
+    b, _, _ = oatt.splitkv_decode(q, kc[perm], vc[perm], inv[table], L, 4, 0.1)
+    np.testing.assert_array_equal(a, b)
+    # the partially filled last page: tokens >= L are ignored
+    kc2 = kc.copy()
+    last = table[L // bs]
+    kc2[last, L % bs:] = 1e4
+    c, _, _ = oatt.splitkv_decode(q, kc2, vc, table, L, 4, 0.1)
+    np.testing.assert_array_equal(a, c)
+
+
+def test_lse_of_single_split_is_logsumexp():
+    rng = np.random.default_rng(4)
+    q, k, v = rand_case(rng, 64)
+    po, pl = oatt.splitkv_partials(q, k, v, 0.3, [(0, 64)])
+    for h in range(8):
+        s = (k[:, h // 4, :].astype(np.float64) @ q[h].astype(np.float64)) * 0.3
+        lse = np.log(np.sum(np.exp(s - s.max()))) + s.max()
+        assert abs(pl[0, h] - lse) < 1e-4

@@ -1,0 +1,153 @@
+"""Pins for the oracle's Q4_0 and bf16 restatements (CPU only).
+
+Known answers come from the GGUF Q4_0 definition (fp16 LE scale, low nibble
+= element j, high nibble = element j + 16, value d * (nibble - 8)) and from
+IEEE 754 binary16 / bfloat16 rounding.  The C and numpy restatements are
+written independently (ldexp decode vs numpy float16) and must agree."""
+import numpy as np
+import pytest
+
+from oracle import q4_0 as oq
+from oracle.bf16 import bf16_bits_to_f32, f32_to_bf16_bits, round_bf16
+
+
+def one_block(d: float, codes) -> np.ndarray:
+    return oq.pack_blocks(np.array([[d]], dtype=np.float16),
+                          np.asarray(codes, dtype=np.uint8).reshape(1, 1, 32))
+
+
+def test_kat_unit_scale_codes():
+    codes = np.arange(32) % 16
+    w = oq.dequant_f32(one_block(1.0, codes), 1, 32)[0]
+    np.testing.assert_array_equal(w, (codes - 8).astype(np.float32))
+
+
+def test_kat_nibble_order():
+    """byte 0 = 0x1F: element 0 = 15 - 8 = 7, element 16 = 1 - 8 = -7."""
+    blk = np.zeros((1, 18), dtype=np.uint8)
+    blk[0, 0:2] = np.array([1.0], dtype="<f2").view(np.uint8)
+    blk[0, 2] = 0x1F
+    blk[0, 3:] = 0x88
+    q, s = oq.unpack(blk, 1, 32)
+    assert q[0, 0] == 7 and q[0, 16] == -7
+    assert np.all(q[0, 1:16] == 0) and np.all(q[0, 17:] == 0)
+    qc, sc = oq.c_unpack(blk, 1, 32)
+    np.testing.assert_array_equal(q, qc)
+    assert s[0, 0] == 1.0 and sc[0, 0] == 1.0
+
+
+@pytest.mark.parametrize("d,expect", [
+    (-0.0, None), (2.0 ** -24, None), (65504.0, None), (np.inf, None), (-np.inf, None)])
+def test_kat_special_scales(d, expect):
+    codes = np.arange(32) % 16
+    blk = one_block(d, codes)
+    w = oq.dequant_f32(blk, 1, 32)[0]
+    wc = oq.c_dequant_f32(blk, 1, 32)[0]
+    with np.errstate(invalid="ignore"):
+        ref = np.float32(d) * (codes - 8).astype(np.float32)
+    np.testing.assert_array_equal(w, ref)
+    np.testing.assert_array_equal(wc, ref)
+    if d == 2.0 ** -24:  # fp16 subnormal times a small integer stays exact
+        assert w[15] == 7 * 2.0 ** -24
+    if np.isinf(d):  # inf * 0 is NaN at code 8
+        assert np.isnan(w[8]) and np.isnan(wc[8])
+
+
+def test_kat_nan_scale_propagates():
+    blk = one_block(np.nan, np.arange(32) % 16)
+    assert np.isnan(oq.dequant_f32(blk, 1, 32)).all()
+    assert np.isnan(oq.c_dequant_f32(blk, 1, 32)).all()
+
+
+def test_c_fp16_decode_matches_numpy_for_every_pattern():
+    lib = oq.c_lib()
+    bits = np.arange(65536, dtype=np.uint16)
+    ref = bits.view(np.float16).astype(np.float32)
+    got = np.array([lib.oracle_f16_to_f32(int(b)) for b in bits[::7]], dtype=np.float32)
+    r = ref[::7]
+    nan = np.isnan(r)
+    np.testing.assert_array_equal(np.isnan(got), nan)
+    np.testing.assert_array_equal(got[~nan], r[~nan])
+
+
+@pytest.mark.parametrize("f,bits", [
+    (1.0, 0x3F80), (1.00390625, 0x3F80),        # tie, even stays
+    (1.01171875, 0x3F82),                        # tie, odd rounds up
+    (1.0078125, 0x3F81), (-2.0, 0xC000),
+    (3.3895313892515355e38, 0x7F7F),             # largest finite bf16
+    (float(np.uint32(0x7F7F8000).view(np.float32)), 0x7F80),  # tie above it -> inf
+    (float("inf"), 0x7F80), (1e-45, 0x0000),
+])
+def test_bf16_rne_known_answers(f, bits):
+    assert int(f32_to_bf16_bits(np.float32([f]))[0]) == bits
+    assert int(oq.c_lib().oracle_f32_to_bf16(f)) == bits
+
+
+def test_bf16_nan_stays_nan():
+    assert np.isnan(bf16_bits_to_f32(f32_to_bf16_bits(np.float32([np.nan])))[0])
+
+
+def test_c_and_numpy_dequant_agree():
+    blocks = oq.make_blocks(64, 512, seed=1)
+    np.testing.assert_array_equal(oq.dequant_f32(blocks, 64, 512), oq.c_dequant_f32(blocks, 64, 512))
+    np.testing.assert_array_equal(oq.dequant_bf16_bits(blocks, 64, 512),
+                                  oq.c_dequant_bf16_bits(blocks, 64, 512))
+    q, s = oq.unpack(blocks, 64, 512)
+    qc, sc = oq.c_unpack(blocks, 64, 512)
+    np.testing.assert_array_equal(q, qc)
+    np.testing.assert_array_equal(s.view(np.uint16), sc.view(np.uint16))
+
+
+def test_generator_recipe():
+    blocks = oq.make_blocks(300, 2560, seed=2)
+    q, s = oq.unpack(blocks, 300, 2560)
+    assert q.min() == -8 and q.max() == 7
+    assert np.all(s >= 0)
+    assert abs(float(np.mean(s.astype(np.float64))) - 0.02 * np.sqrt(2 / np.pi)) < 5e-4
+
+
+def test_gemv_f64_matches_brute_force():
+    rng = np.random.default_rng(0)
+    n, k = 16, 128
+    blocks = oq.make_blocks(n, k, seed=4)
+    x = f32_to_bf16_bits(rng.standard_normal(k).astype(np.float32))
+    xf = bf16_bits_to_f32(x).astype(np.float64)
+    q, s = oq.unpack(blocks, n, k)
+    brute = np.zeros(n)
+    for r in range(n):
+        for j in range(k):
+            brute[r] += float(s[r, j // 32]) * float(q[r, j]) * xf[j]
+    np.testing.assert_allclose(oq.gemv_f64(x, blocks, n, k), brute, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(oq.gemv_np_f64(xf, blocks, n, k), brute, rtol=1e-12, atol=1e-12)
+
+
+def test_gemv_one_hot_and_linearity_and_zero_scale():
+    n, k = 32, 256
+    blocks = oq.make_blocks(n, k, seed=5)
+    w = oq.dequant_f32(blocks, n, k)
+    e = np.zeros(k, dtype=np.uint16)
+    e[37] = 0x3F80
+    np.testing.assert_array_equal(oq.gemv_f64(e, blocks, n, k), w[:, 37].astype(np.float64))
+    rng = np.random.default_rng(1)
+    a = f32_to_bf16_bits(rng.standard_normal(k).astype(np.float32))
+    b = f32_to_bf16_bits(rng.standard_normal(k).astype(np.float32))
+    a[::2] = 0  # disjoint supports make a + b exact in bf16
+    b[1::2] = 0
+    ab = a | b
+    np.testing.assert_allclose(oq.gemv_f64(ab, blocks, n, k),
+                               oq.gemv_f64(a, blocks, n, k) + oq.gemv_f64(b, blocks, n, k),
+                               rtol=1e-12, atol=1e-9)
+    zero = blocks.copy().reshape(n, k // 32, 18)
+    zero[:, :, 0:2] = 0
+    assert not oq.gemv_f64(a, zero.reshape(n, -1), n, k).any()
+
+
+def test_gemv_bf16_weight_variant_close_to_exact():
+    rng = np.random.default_rng(3)
+    n, k = 64, 2560
+    blocks = oq.make_blocks(n, k, seed=6)
+    x = f32_to_bf16_bits(rng.standard_normal(k).astype(np.float32))
+    exact = oq.gemv_f64(x, blocks, n, k)
+    ref = bf16_bits_to_f32(oq.gemv_bf16w_bits(x, blocks, n, k))
+    assert np.max(np.abs(ref - exact) / (np.abs(exact) + 0.05)) < 2e-2
+    assert np.array_equal(round_bf16(np.float32([1.5])), np.float32([1.5]))
