@@ -86,6 +86,46 @@ int smx_q4_0_gemv_swiglu(void* stream, const void* x, const void* w,
                          void* out, int64_t d, int64_t k);
 
 /*
+ * Q4_0 GEMV whose activation is RMSNorm(x + residual) * gamma, computed by
+ * the GEMV itself (norm_ub semantics, as smx_add_rmsnorm):
+ *   s = float(x) + float(residual)  (residual may be NULL)
+ *   a = RNE_bf16(s / sqrt(mean(s^2) + eps) * gamma);  y = W a  (bf16)
+ * and, when residual_out != NULL, residual_out = RNE_bf16(s).
+ * residual_out must not alias x or residual (other workgroups still read
+ * them).  k % 64 == 0, k <= 65536; x, residual, gamma, residual_out 16-byte
+ * aligned, w 4-byte aligned.  Fuses the reference's add+RMSNorm with the
+ * following projection (NativeUp.execute: norm_ub then the gate/up GEMV,
+ * src/spark_vllm_ascend/kernels/linear.py:585-611).
+ */
+int smx_q4_0_add_rmsnorm_gemv(void* stream, const void* x, const void* residual,
+                              const void* gamma, void* residual_out,
+                              const void* w, void* y, int64_t n, int64_t k,
+                              float eps);
+
+/* smx_q4_0_add_rmsnorm_gemv followed by the SwiGLU of smx_q4_0_gemv_swiglu:
+ * w is [2*d, k] (gate rows then up rows), out is [d]. */
+int smx_q4_0_add_rmsnorm_gemv_swiglu(void* stream, const void* x,
+                                     const void* residual, const void* gamma,
+                                     void* residual_out, const void* w,
+                                     void* out, int64_t d, int64_t k,
+                                     float eps);
+
+/*
+ * smx_q4_0_add_rmsnorm_gemv for the LM head (no residual_out) that also
+ * leaves greedy-argmax keys: one uint64 per workgroup in keys[num_keys],
+ * reduced by smx_decode_advance.  num_keys must equal
+ * smx_q4_0_argmax_keys_size(n, k) (-1 for an unsupported shape).  Replaces
+ * the head GEMV + sampler pair (src/spark_vllm_ascend/integration/
+ * head.py:13-16 and vLLM's greedy sampler).
+ */
+int64_t smx_q4_0_argmax_keys_size(int64_t n, int64_t k);
+int smx_q4_0_add_rmsnorm_gemv_argmax(void* stream, const void* x,
+                                     const void* residual, const void* gamma,
+                                     const void* w, void* logits,
+                                     uint64_t* keys, int64_t num_keys,
+                                     int64_t n, int64_t k, float eps);
+
+/*
  * Split-KV flash-decode attention, one partial per (sequence, split, q head).
  *   q: [num_seqs, n_q, head_dim] bf16
  *   k_cache, v_cache: [num_blocks, block_size, n_kv, head_dim] bf16
@@ -127,6 +167,27 @@ int smx_splitkv_decode_merged(void* stream, const void* q, const void* k_cache,
                               int32_t num_splits, int32_t max_blocks,
                               int32_t num_blocks, int32_t block_size, int32_t n_q,
                               int32_t n_kv, int32_t head_dim, float scale);
+
+/*
+ * smx_qknorm_rope_kv_write fused into smx_splitkv_decode_merged, for one
+ * decode token per sequence: qkv is the raw QKV projection
+ * [num_seqs, (n_q + 2*n_kv) * head_dim]; every workgroup applies the
+ * per-head q RMSNorm (q_gamma) + neox RoPE at positions[r] to its own q
+ * heads, and the workgroup whose split holds positions[r] applies the k norm
+ * + RoPE to the new token, writes K/V to the cache at slot_mapping[r] and
+ * uses them directly.  positions[r] must be seq_lens[r] - 1 (the decode
+ * token is the last of its sequence).  Replaces the reference's fused
+ * QKV-stage RoPE/KV write feeding AttentionStage
+ * (src/spark_vllm_ascend/kernels/qkv.py:179-236, kernels/attention.py).
+ */
+int smx_qknorm_rope_splitkv_decode_merged(
+    void* stream, const void* qkv, const void* q_gamma, const void* k_gamma,
+    const void* cos_sin, const int64_t* positions, const int64_t* slot_mapping,
+    void* k_cache, void* v_cache, const int32_t* block_table,
+    const int32_t* seq_lens, float* partial_o, float* partial_lse, void* out,
+    int32_t num_seqs, int32_t num_splits, int32_t max_blocks,
+    int32_t num_blocks, int32_t block_size, int32_t n_q, int32_t n_kv,
+    int32_t head_dim, int32_t max_position, float eps, float scale);
 
 /*
  * Log-sum-exp merge of the split partials:
@@ -218,6 +279,8 @@ int smx_reshape_and_cache(void* stream, const void* key, const void* value,
 /*
  * Advance a decode batch by one token, on the device, so that one captured
  * graph serves every step (prompt ingestion and generation):
+ *   if argmax_keys != NULL: next_ids[r] = argmax from the num_keys keys of
+ *       row r written by smx_q4_0_add_rmsnorm_gemv_argmax;
  *   p = positions[r] + 1;
  *   ids[r] = forced_ids[r, p] if forced_ids != NULL and p < forced_len[r]
  *            else next_ids[r];
@@ -231,7 +294,8 @@ int smx_reshape_and_cache(void* stream, const void* key, const void* value,
  * formula is the reference's slot mapping
  * (src/spark_vllm_ascend/integration/slot_mapping.py:8-33).
  */
-int smx_decode_advance(void* stream, const int64_t* next_ids,
+int smx_decode_advance(void* stream, int64_t* next_ids,
+                       const uint64_t* argmax_keys, int32_t num_keys,
                        const int64_t* forced_ids, const int32_t* forced_len,
                        int64_t* ids, int64_t* positions, int32_t* seq_lens,
                        int64_t* slot_mapping, const int32_t* block_table,

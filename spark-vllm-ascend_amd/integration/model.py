@@ -8,16 +8,23 @@ spark2_5.py:369-376), with the last layer's "next norm" being the model's
 final norm (integration/model.py:88-92).  vLLM captures the whole step in
 one device graph (src/tools/deployment/serve.py:34).
 
-Here one decode step is the kernel sequence
+Here one decode step is the kernel sequence (fused=True, the default)
 
-  embedding -> RMSNorm(input_norm[0])
-  per layer:  QKV Q4_0 GEMV -> q/k RMSNorm + RoPE + KV write
-              -> split-KV attention -> LSE merge -> o_proj Q4_0 GEMV
-              -> add + RMSNorm(post_attention_norm)
-              -> gate|up Q4_0 GEMV with SwiGLU -> down Q4_0 GEMV
-              -> add + RMSNorm(next layer's input_norm or the final norm)
-  head Q4_0 GEMV -> argmax -> on-device advance (next input id, position,
-              sequence length, KV slot)
+  embedding
+  per layer:  add + RMSNorm(input_norm) fused into the QKV Q4_0 GEMV
+              -> q/k RMSNorm + RoPE + KV write fused into split-KV attention
+              -> LSE merge -> o_proj Q4_0 GEMV
+              -> add + RMSNorm(post_attention_norm) fused into the gate|up
+                 Q4_0 GEMV with SwiGLU -> down Q4_0 GEMV
+  add + RMSNorm(final norm) fused into the head Q4_0 GEMV, whose workgroups
+  also leave per-workgroup argmax keys -> on-device advance (reduces the keys
+  to the next input id; position, sequence length, KV slot)
+
+i.e. 6 launches per layer.  Each layer hands (down output, residual) to the
+next, whose first GEMV adds and normalises them (the reference's "next norm"
+at the end of a layer, moved to the consumer).  fused=False runs the same
+math as separate launches (add_rmsnorm, GEMV, q/k-norm kernel, attention,
+argmax), 9 per layer.
 
 captured once as a torch.cuda.CUDAGraph (a hipGraph).  Position, sequence
 length and slot are read from device memory by the kernels, as the
@@ -102,8 +109,10 @@ class DecodeModel:
     """A batch-1 Q4_0 decoder with random-init weights of a given shape."""
 
     def __init__(self, cfg: DecoderConfig, device, seed: int = 0, max_len: int = 8192,
-                 num_splits: int | None = None, weights: dict | None = None):
+                 num_splits: int | None = None, weights: dict | None = None,
+                 fused: bool = True):
         self.cfg = cfg
+        self.fused = fused
         self.device = torch.device(device)
         self.max_len = max_len
         c = cfg
@@ -163,53 +172,86 @@ class DecodeModel:
         )
         # activations (fixed addresses for graph capture)
         bf = dict(dtype=torch.bfloat16, device=dev)
-        self.x = torch.empty((1, c.hidden), **bf)         # embedding / residual stream
-        self.h = torch.empty((1, c.hidden), **bf)         # normalised layer input
+        self.x = torch.empty((1, c.hidden), **bf)         # embedding of the input id
+        self.res_a = torch.empty((1, c.hidden), **bf)     # residual after the attention add
+        self.res_b = torch.empty((1, c.hidden), **bf)     # residual after the MLP add
+        self.d = torch.empty((1, c.hidden), **bf)         # down projection output
+        self.h = torch.empty((1, c.hidden), **bf)         # normalised input (fused=False)
         self.qkv_out = torch.empty((1, c.qkv_rows), **bf)
         self.q = torch.empty((1, c.n_q, c.head_dim), **bf)
         self.attn = torch.empty((1, c.n_q, c.head_dim), **bf)
         self.o = torch.empty((1, c.hidden), **bf)
         self.h2 = torch.empty((1, c.hidden), **bf)
         self.act = torch.empty((1, c.intermediate), **bf)
-        self.down_out = torch.empty((1, c.hidden), **bf)
         self.logits = torch.empty((1, c.vocab), **bf)
         self.partial_o = torch.empty((1, self.num_splits, c.n_q, c.head_dim), dtype=torch.float32,
                                      device=dev)
         self.partial_lse = torch.empty((1, self.num_splits, c.n_q), dtype=torch.float32, device=dev)
+        nk = torch_ops.argmax_keys_size(c.vocab, c.hidden)
+        self.argmax_keys = (torch.empty((1, nk), dtype=torch.int64, device=dev) if nk > 0
+                            else None)
         self.graph: torch.cuda.CUDAGraph | None = None
 
     # ------------------------------------------------------------------ step
+    def _layer_input(self, i: int):
+        """(activation, residual) entering layer i: the embedding alone for
+        layer 0, else the previous layer's down output and residual."""
+        return (self.x, None) if i == 0 else (self.d, self.res_b)
+
     def layer_run(self, i: int) -> None:
-        """One decoder layer on (self.h, self.x): leaves the next layer's
-        normalised input in self.h and the residual stream in self.x."""
+        """Decoder layer i: reads _layer_input(i), leaves the down projection
+        in self.d and the residual stream in self.res_b (the next consumer
+        adds and normalises them)."""
         c, L, st = self.cfg, self.layers[i], self.state
         ops = torch_ops
-        ops.q4_0_gemv(self.h, L.qkv.qweight, c.qkv_rows, c.hidden, out=self.qkv_out)
-        ops.qknorm_rope_kv_write(self.qkv_out, L.q_norm, L.k_norm, self.cos_sin, st.positions,
-                                 st.slot_mapping, L.kv_cache[0], L.kv_cache[1], c.n_q, c.n_kv,
-                                 c.eps, q_out=self.q)
-        ops.splitkv_decode_merged(self.q, L.kv_cache[0], L.kv_cache[1], st.block_table,
-                                  st.seq_lens, self.num_splits, self.scale, self.partial_o,
-                                  self.partial_lse, out=self.attn)
-        ops.q4_0_gemv(self.attn, L.o_proj.qweight, c.hidden, c.n_q * c.head_dim, out=self.o)
-        ops.add_rmsnorm(self.o, self.x, L.post_norm, c.eps, out=self.h2, residual_out=self.x)
-        ops.q4_0_gemv_swiglu(self.h2, L.gate_up.qweight, c.intermediate, c.hidden, out=self.act)
-        ops.q4_0_gemv(self.act, L.down.qweight, c.hidden, c.intermediate, out=self.down_out)
-        nxt = self.layers[i + 1].input_norm if i + 1 < len(self.layers) else self.final_norm
-        ops.add_rmsnorm(self.down_out, self.x, nxt, c.eps, out=self.h, residual_out=self.x)
+        x_in, r_in = self._layer_input(i)
+        if self.fused:
+            ops.add_rmsnorm_gemv(x_in, r_in, L.input_norm, L.qkv.qweight, c.qkv_rows, c.hidden,
+                                 c.eps, residual_out=self.res_a, out=self.qkv_out)
+            ops.qknorm_rope_splitkv_decode_merged(
+                self.qkv_out, L.q_norm, L.k_norm, self.cos_sin, st.positions, st.slot_mapping,
+                L.kv_cache[0], L.kv_cache[1], st.block_table, st.seq_lens, self.num_splits,
+                self.scale, c.eps, c.n_q, self.partial_o, self.partial_lse, out=self.attn)
+            ops.q4_0_gemv(self.attn, L.o_proj.qweight, c.hidden, c.n_q * c.head_dim, out=self.o)
+            ops.add_rmsnorm_gemv_swiglu(self.o, self.res_a, L.post_norm, L.gate_up.qweight,
+                                        c.intermediate, c.hidden, c.eps, residual_out=self.res_b,
+                                        out=self.act)
+        else:
+            ops.add_rmsnorm(x_in, r_in, L.input_norm, c.eps, out=self.h, residual_out=self.res_a)
+            ops.q4_0_gemv(self.h, L.qkv.qweight, c.qkv_rows, c.hidden, out=self.qkv_out)
+            ops.qknorm_rope_kv_write(self.qkv_out, L.q_norm, L.k_norm, self.cos_sin, st.positions,
+                                     st.slot_mapping, L.kv_cache[0], L.kv_cache[1], c.n_q, c.n_kv,
+                                     c.eps, q_out=self.q)
+            ops.splitkv_decode_merged(self.q, L.kv_cache[0], L.kv_cache[1], st.block_table,
+                                      st.seq_lens, self.num_splits, self.scale, self.partial_o,
+                                      self.partial_lse, out=self.attn)
+            ops.q4_0_gemv(self.attn, L.o_proj.qweight, c.hidden, c.n_q * c.head_dim, out=self.o)
+            ops.add_rmsnorm(self.o, self.res_a, L.post_norm, c.eps, out=self.h2,
+                            residual_out=self.res_b)
+            ops.q4_0_gemv_swiglu(self.h2, L.gate_up.qweight, c.intermediate, c.hidden,
+                                 out=self.act)
+        ops.q4_0_gemv(self.act, L.down.qweight, c.hidden, c.intermediate, out=self.d)
 
     def enqueue_step(self) -> None:
         c, st = self.cfg, self.state
         ops = torch_ops
         self.head.embed(st.ids, out=self.x)
-        ops.add_rmsnorm(self.x, None, self.layers[0].input_norm, c.eps, out=self.h)
         for i in range(len(self.layers)):
             self.layer_run(i)
-        ops.q4_0_gemv(self.h, self.head.q4_0_head, c.vocab, c.hidden, out=self.logits)
-        ops.argmax(self.logits, out=st.next_ids)
+        x_in, r_in = self._layer_input(len(self.layers))
+        keys = None
+        if self.fused and self.argmax_keys is not None:
+            ops.add_rmsnorm_gemv_argmax(x_in, r_in, self.final_norm, self.head.q4_0_head,
+                                        c.vocab, c.hidden, c.eps, self.argmax_keys.view(-1),
+                                        out=self.logits)
+            keys = self.argmax_keys
+        else:
+            ops.add_rmsnorm(x_in, r_in, self.final_norm, c.eps, out=self.h)
+            ops.q4_0_gemv(self.h, self.head.q4_0_head, c.vocab, c.hidden, out=self.logits)
+            ops.argmax(self.logits, out=st.next_ids)
         ops.decode_advance(st.next_ids, st.ids, st.positions, st.seq_lens, st.slot_mapping,
                            st.block_table, c.block_size, tokens_out=st.tokens,
-                           forced_ids=st.forced, forced_len=st.forced_len)
+                           forced_ids=st.forced, forced_len=st.forced_len, argmax_keys=keys)
 
     def capture(self) -> None:
         """Capture one decode step as a graph.  Clobbers the decode state;

@@ -35,6 +35,9 @@ SIGNATURES = {
                            _I32, _I32, _F32],
     "smx_splitkv_decode_merged": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32,
                                   _I32, _I32, _I32, _I32, _F32],
+    "smx_qknorm_rope_splitkv_decode_merged": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                              _P, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32,
+                                              _I32, _F32, _F32],
     "smx_lse_merge": [_P, _P, _P, _P, _I32, _I32, _I32, _I32],
     "smx_add_rmsnorm": [_P, _P, _P, _P, _P, _P, _I64, _I64, _F32],
     "smx_qknorm_rope_kv_write": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32,
@@ -43,8 +46,16 @@ SIGNATURES = {
     "smx_embedding": [_P, _P, _P, _P, _I64, _I64, _I64],
     "smx_argmax_bf16": [_P, _P, _I64, _I64, _P],
     "smx_reshape_and_cache": [_P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32],
-    "smx_decode_advance": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32],
+    "smx_decode_advance": [_P, _P, _P, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32,
+                           _I32],
+    "smx_q4_0_add_rmsnorm_gemv": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _F32],
+    "smx_q4_0_add_rmsnorm_gemv_swiglu": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _F32],
+    "smx_q4_0_add_rmsnorm_gemv_argmax": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _F32],
+    "smx_q4_0_argmax_keys_size": [_I64, _I64],
 }
+
+# return types other than int
+RESTYPES = {"smx_q4_0_argmax_keys_size": ctypes.c_int64}
 
 _lib = None
 
@@ -74,7 +85,7 @@ def load() -> ctypes.CDLL:
     for name, argtypes in SIGNATURES.items():
         fn = getattr(lib, name)
         fn.argtypes = argtypes
-        fn.restype = ctypes.c_int
+        fn.restype = RESTYPES.get(name, ctypes.c_int)
     lib.smx_last_error.argtypes = []
     lib.smx_last_error.restype = ctypes.c_char_p
     version = lib.smx_abi_version()

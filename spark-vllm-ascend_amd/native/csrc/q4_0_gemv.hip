@@ -24,6 +24,8 @@
 //    sum x*(n-8); the -136*sum(x) bias depends on x only and is computed once
 //    during staging.  The block sum is scaled by d in fp32, and the 8 lanes
 //    of a row are reduced with DPP.
+#include <math.h>
+
 #include "smx_common.h"
 
 namespace smx {
@@ -89,50 +91,82 @@ __device__ __forceinline__ float pair_dot(const Pair& w, const u32x4* xs, float 
   return acc;
 }
 
+// Order-preserving 16-bit key of a bf16 value (NaN above +inf).
+__device__ __forceinline__ uint32_t bf16_order_key(uint16_t b) {
+  if ((b & 0x7f80u) == 0x7f80u && (b & 0x7fu)) return 0xffffu;  // NaN
+  return (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
+}
+
+enum { EPI_STORE = 0, EPI_SWIGLU = 1, EPI_ARGMAX = 2 };
+
+struct GemvArgs {
+  const uint16_t* x;         // activation (raw input when PRO: the GEMV's own add+RMSNorm)
+  const uint16_t* residual;  // PRO: added to x before the norm (may be null)
+  const uint16_t* gamma;     // PRO: norm weight
+  uint16_t* residual_out;    // PRO: bf16(x + residual), written by workgroup 0 (may be null)
+  const uint8_t* w;
+  uint16_t* y;
+  uint64_t* argmax_keys;     // EPI_ARGMAX: one key per workgroup
+  int n_out;
+  int npairs;
+  int64_t up_offset_rows;
+  float eps;
+};
+
 // One workgroup owns RG groups of 8 weight rows.  Its waves split the K
 // dimension: pair group g (pairs 8g..8g+7) belongs to wave g % ks, and lane
-// 8r+c of a wave handles pair 8g+c of row r.  Each wave stages only the
-// activations of its own pair groups into a private LDS slice, so no
-// workgroup barrier separates the weight loads from the arithmetic; the ks
-// partial sums of a row meet in LDS at the end.  SWIGLU: rows 0-3 of a group
-// are gate rows, rows 4-7 the matching up rows, and the output is
-// silu(gate) * up for 4 features per group.
-template <int NPMAX, int RG, bool SWIGLU>
-__global__ __launch_bounds__(512) void q4_0_gemv_kernel(
-    const uint16_t* __restrict__ x, const uint8_t* __restrict__ w,
-    uint16_t* __restrict__ y, int n_out, int npairs, int64_t up_offset_rows) {
+// 8r+c of a wave handles pair 8g+c of row r.  Each wave stages the
+// activations of its own pair groups into a private LDS slice; the ks
+// partial sums of a row meet in LDS at the end.
+//  PRO: the staged activation is RMSNorm(x + residual) * gamma, computed in
+//       the prologue (the workgroup's waves together read every element once
+//       and reduce the sum of squares through LDS; workgroup 0 also writes the
+//       new residual), which replaces a separate add+RMSNorm launch.
+//  EPI_SWIGLU: rows 0-3 of a group are gate rows, rows 4-7 the matching up
+//       rows, and the output is silu(gate) * up for 4 features per group.
+//  EPI_ARGMAX: besides y, each workgroup writes the max (value, -index) key
+//       of its rows, for an on-device greedy argmax.
+template <int NPMAX, int RG, bool PRO, int EPI>
+__global__ __launch_bounds__(512) void q4_0_gemv_kernel(GemvArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+  constexpr bool SWIGLU = EPI == EPI_SWIGLU;
   const int ks = blockDim.x >> 6;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int col = lane & 7;
   const int rsub = lane >> 3;
+  const int npairs = a.npairs;
+  const int n_out = a.n_out;
   const int64_t row_bytes = (int64_t)npairs * 36;
   const int nchunks = npairs * 8;
   uint32_t* xs = lds + wave * (NPMAX * 8 * 36);
   float* part = reinterpret_cast<float*>(lds + ks * (NPMAX * 8 * 36));
 
   // 1. This wave's activation chunks (16 bytes each, one per lane per group).
-  u32x4 xv[NPMAX];
-  const u32x4* xg = reinterpret_cast<const u32x4*>(x);
+  u32x4 xv[NPMAX], rv[NPMAX], gv[NPMAX];
+  const u32x4* xg = reinterpret_cast<const u32x4*>(a.x);
 #pragma unroll
   for (int t = 0; t < NPMAX; ++t) {
     const int c = (wave + ks * t) * 64 + lane;
-    xv[t] = c < nchunks ? xg[c] : u32x4{0u, 0u, 0u, 0u};
+    const bool ok = c < nchunks;
+    xv[t] = ok ? xg[c] : u32x4{0u, 0u, 0u, 0u};
+    if constexpr (PRO) {
+      rv[t] = ok && a.residual ? reinterpret_cast<const u32x4*>(a.residual)[c]
+                               : u32x4{0u, 0u, 0u, 0u};
+      gv[t] = ok ? reinterpret_cast<const u32x4*>(a.gamma)[c] : u32x4{0u, 0u, 0u, 0u};
+    }
   }
 
   // 2. Every weight load of this wave.
   constexpr int OUT_PER_GROUP = SWIGLU ? 4 : 8;
-  int out_idx[RG];
   int64_t wrow[RG];
   bool row_ok[RG];
 #pragma unroll
   for (int g = 0; g < RG; ++g) {
     const int o = (blockIdx.x * RG + g) * OUT_PER_GROUP + (SWIGLU ? (rsub & 3) : rsub);
-    out_idx[g] = o;
     row_ok[g] = o < n_out;
-    wrow[g] = SWIGLU ? (o + ((rsub >> 2) ? up_offset_rows : 0)) : o;
+    wrow[g] = SWIGLU ? (o + ((rsub >> 2) ? a.up_offset_rows : 0)) : o;
   }
   Pair wp[RG][NPMAX];
 #pragma unroll
@@ -141,7 +175,7 @@ __global__ __launch_bounds__(512) void q4_0_gemv_kernel(
     for (int t = 0; t < NPMAX; ++t) {
       const int j = (wave + ks * t) * 8 + col;
       if (row_ok[g] && j < npairs) {
-        wp[g][t] = load_pair(w + wrow[g] * row_bytes + 36 * j);
+        wp[g][t] = load_pair(a.w + wrow[g] * row_bytes + 36 * j);
       } else {
         wp[g][t].a = u32x4{0u, 0u, 0u, 0u};
         wp[g][t].b = u32x4{0u, 0u, 0u, 0u};
@@ -150,7 +184,48 @@ __global__ __launch_bounds__(512) void q4_0_gemv_kernel(
     }
   }
 
-  // 3. Stage the activations as 36-dword pair records with the block biases
+  // 3. PRO: residual add + RMSNorm of the activation (norm_ub semantics:
+  //    src/spark_vllm_ascend/kernels/linear.py:202-224).
+  if constexpr (PRO) {
+    float sv[NPMAX][8];
+    float ss = 0.f;
+#pragma unroll
+    for (int t = 0; t < NPMAX; ++t) {
+      const uint32_t xw[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
+      const uint32_t rw[4] = {rv[t].x, rv[t].y, rv[t].z, rv[t].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sv[t][2 * i] = bf16_lo(xw[i]) + bf16_lo(rw[i]);
+        sv[t][2 * i + 1] = bf16_hi(xw[i]) + bf16_hi(rw[i]);
+        ss += sv[t][2 * i] * sv[t][2 * i] + sv[t][2 * i + 1] * sv[t][2 * i + 1];
+      }
+    }
+    ss = wave_sum(ss);
+    float* red = part + ks * 8 * RG;
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    float tot = 0.f;
+    for (int i = 0; i < ks; ++i) tot += red[i];
+    const float inv = 1.0f / sqrtf(tot / (float)(nchunks * 8) + a.eps);
+    const bool write_res = blockIdx.x == 0 && a.residual_out;
+#pragma unroll
+    for (int t = 0; t < NPMAX; ++t) {
+      const uint32_t gw[4] = {gv[t].x, gv[t].y, gv[t].z, gv[t].w};
+      uint32_t yo[4], ro[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float s0 = sv[t][2 * i], s1 = sv[t][2 * i + 1];
+        ro[i] = pack_bf16x2(s0, s1);
+        yo[i] = pack_bf16x2(s0 * inv * bf16_lo(gw[i]), s1 * inv * bf16_hi(gw[i]));
+      }
+      xv[t] = u32x4{yo[0], yo[1], yo[2], yo[3]};
+      const int c = (wave + ks * t) * 64 + lane;
+      if (write_res && c < nchunks)
+        reinterpret_cast<u32x4*>(a.residual_out)[c] = u32x4{ro[0], ro[1], ro[2], ro[3]};
+    }
+  }
+
+  // 4. Stage the activations as 36-dword pair records with the block biases
   //    -136 * sum(x_block).  The four chunks of a block sit in one lane quad.
 #pragma unroll
   for (int t = 0; t < NPMAX; ++t) {
@@ -171,7 +246,7 @@ __global__ __launch_bounds__(512) void q4_0_gemv_kernel(
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-  // 4. Dot products, consuming the weights in issue order.
+  // 5. Dot products, consuming the weights in issue order.
   float acc[RG];
 #pragma unroll
   for (int g = 0; g < RG; ++g) acc[g] = 0.f;
@@ -185,30 +260,45 @@ __global__ __launch_bounds__(512) void q4_0_gemv_kernel(
     }
   }
 
-  // 5. Row sums: 8 lanes by DPP, then the ks waves through LDS.
+  // 6. Row sums: 8 lanes by DPP, then the ks waves through LDS.
 #pragma unroll
   for (int g = 0; g < RG; ++g) {
     const float v = sum8(acc[g]);
     if (col == 0) part[wave * (8 * RG) + g * 8 + rsub] = v;
   }
   __syncthreads();
-  if (wave == 0 && lane < 8 * RG) {
-    const int g = lane >> 3;
-    const int r = lane & 7;
-    float tot = 0.f;
-    for (int i = 0; i < ks; ++i) tot += part[i * (8 * RG) + lane];
-    if constexpr (SWIGLU) {
-      const int o = (blockIdx.x * RG + g) * 4 + r;
-      if (r < 4 && o < n_out) {
-        float up = 0.f;
-        for (int i = 0; i < ks; ++i) up += part[i * (8 * RG) + g * 8 + r + 4];
-        const float gb = round_bf16(tot);
-        const float ub = round_bf16(up);
-        y[o] = f32_to_bf16(gb / (1.0f + expf(-gb)) * ub);
+  if (wave == 0) {
+    uint64_t key = 0;
+    if (lane < 8 * RG) {
+      const int g = lane >> 3;
+      const int r = lane & 7;
+      float tot = 0.f;
+      for (int i = 0; i < ks; ++i) tot += part[i * (8 * RG) + lane];
+      if constexpr (SWIGLU) {
+        const int o = (blockIdx.x * RG + g) * 4 + r;
+        if (r < 4 && o < n_out) {
+          float up = 0.f;
+          for (int i = 0; i < ks; ++i) up += part[i * (8 * RG) + g * 8 + r + 4];
+          const float gb = round_bf16(tot);
+          const float ub = round_bf16(up);
+          a.y[o] = f32_to_bf16(gb / (1.0f + expf(-gb)) * ub);
+        }
+      } else {
+        const int o = (blockIdx.x * RG + g) * 8 + r;
+        if (o < n_out) {
+          const uint16_t yb = f32_to_bf16(tot);
+          a.y[o] = yb;
+          key = ((uint64_t)bf16_order_key(yb) << 32) | (uint64_t)(0xffffffffu - (uint32_t)o);
+        }
       }
-    } else {
-      const int o = (blockIdx.x * RG + g) * 8 + r;
-      if (o < n_out) y[o] = f32_to_bf16(tot);
+    }
+    if constexpr (EPI == EPI_ARGMAX) {
+      for (int m = 1; m < 64; m <<= 1) {
+        const uint64_t other = ((uint64_t)(uint32_t)__shfl_xor((int)(key >> 32), m, 64) << 32) |
+                               (uint32_t)__shfl_xor((int)(uint32_t)key, m, 64);
+        key = other > key ? other : key;
+      }
+      if (lane == 0) a.argmax_keys[blockIdx.x] = key;
     }
   }
 }
@@ -286,15 +376,13 @@ __global__ __launch_bounds__(256) void q4_0_dequant_kernel(
 // Host launchers.
 // ---------------------------------------------------------------------------
 
-template <int NPMAX, int RG, bool SWIGLU>
-static hipError_t launch_fast(hipStream_t s, const void* x, const void* w, void* y, int n_out,
-                              int npairs, int64_t up_rows, int ks) {
-  constexpr int OUT_PER_WG = (SWIGLU ? 4 : 8) * RG;
-  const int grid = (n_out + OUT_PER_WG - 1) / OUT_PER_WG;
-  const size_t lds = (size_t)ks * NPMAX * 8 * 36 * 4 + (size_t)ks * 8 * RG * 4;
-  hipLaunchKernelGGL((q4_0_gemv_kernel<NPMAX, RG, SWIGLU>), dim3(grid), dim3(64 * ks), lds, s,
-                     (const uint16_t*)x, (const uint8_t*)w, (uint16_t*)y, n_out, npairs,
-                     up_rows);
+template <int NPMAX, int RG, bool PRO, int EPI>
+static hipError_t launch_fast(hipStream_t s, const GemvArgs& a, int ks) {
+  constexpr int OUT_PER_WG = (EPI == EPI_SWIGLU ? 4 : 8) * RG;
+  const int grid = (a.n_out + OUT_PER_WG - 1) / OUT_PER_WG;
+  const size_t lds = (size_t)ks * NPMAX * 8 * 36 * 4 + (size_t)ks * 8 * RG * 4 + (size_t)ks * 4;
+  hipLaunchKernelGGL((q4_0_gemv_kernel<NPMAX, RG, PRO, EPI>), dim3(grid), dim3(64 * ks), lds, s,
+                     a);
   return hipGetLastError();
 }
 
@@ -318,7 +406,7 @@ static GemvShape pick_shape(int n_out, int out_per_group, int ngroups) {
   const char* e = getenv("SMX_GEMV_SHAPE");  // "rg,ks" override for tuning sweeps
   if (e) {
     int a = 0, b = 0;
-    if (sscanf(e, "%d,%d", &a, &b) == 2 && (a == 1 || a == 2 || a == 4) && b >= 1 && b <= 8) {
+    if (sscanf(e, "%d,%d", &a, &b) == 2 && (a == 1 || a == 2) && b >= 1 && b <= 8) {
       sh.rg = a;
       sh.ks = b < ngroups ? b : ngroups;
       sh.np = (ngroups + sh.ks - 1) / sh.ks;
@@ -327,54 +415,65 @@ static GemvShape pick_shape(int n_out, int out_per_group, int ngroups) {
   return sh;
 }
 
-template <int NPMAX, bool SWIGLU>
-static hipError_t dispatch_rg(hipStream_t s, const void* x, const void* w, void* y, int n_out,
-                              int npairs, int64_t up_rows, const GemvShape& sh) {
-  if (sh.rg == 4) return launch_fast<NPMAX, 4, SWIGLU>(s, x, w, y, n_out, npairs, up_rows, sh.ks);
-  if (sh.rg == 2) return launch_fast<NPMAX, 2, SWIGLU>(s, x, w, y, n_out, npairs, up_rows, sh.ks);
-  return launch_fast<NPMAX, 1, SWIGLU>(s, x, w, y, n_out, npairs, up_rows, sh.ks);
+template <int NPMAX, bool PRO, int EPI>
+static hipError_t dispatch_rg(hipStream_t s, const GemvArgs& a, const GemvShape& sh) {
+  if (sh.rg == 2) return launch_fast<NPMAX, 2, PRO, EPI>(s, a, sh.ks);
+  return launch_fast<NPMAX, 1, PRO, EPI>(s, a, sh.ks);
 }
 
-static hipError_t gemv_dispatch(hipStream_t s, const void* x, const void* w, void* y,
-                                int64_t n_out, int64_t k, bool swiglu) {
-  const int64_t nblocks = k / 32;
-  const int npairs = (int)(nblocks / 2);
-  const int ngroups = (npairs + 7) / 8;
-  const int64_t up_rows = swiglu ? n_out : 0;
-  GemvShape sh{1, 1, 1};
-  bool fast = (k % 64 == 0) && ((uintptr_t)w % 4 == 0) && ((uintptr_t)x % 16 == 0);
-  if (fast) {
-    sh = pick_shape((int)n_out, swiglu ? 4 : 8, ngroups);
-    fast = sh.np <= 8;
+template <bool PRO, int EPI>
+static hipError_t dispatch_np(hipStream_t s, const GemvArgs& a, const GemvShape& sh) {
+  switch (sh.np) {
+    case 1: return dispatch_rg<1, PRO, EPI>(s, a, sh);
+    case 2: return dispatch_rg<2, PRO, EPI>(s, a, sh);
+    case 3: return dispatch_rg<3, PRO, EPI>(s, a, sh);
+    case 4: return dispatch_rg<4, PRO, EPI>(s, a, sh);
+    case 5: return dispatch_rg<5, PRO, EPI>(s, a, sh);
+    case 6: return dispatch_rg<6, PRO, EPI>(s, a, sh);
+    case 7: return dispatch_rg<7, PRO, EPI>(s, a, sh);
+    case 8: return dispatch_rg<8, PRO, EPI>(s, a, sh);
+    default: return hipErrorInvalidValue;
   }
-  if (!fast) {
-    if (swiglu)
-      hipLaunchKernelGGL(q4_0_gemv_generic_kernel<true>, dim3((unsigned)n_out), dim3(64), 0, s,
-                         (const uint16_t*)x, (const uint8_t*)w, (uint16_t*)y, (int)n_out,
-                         (int)nblocks, up_rows);
+}
+
+// Whether the streaming kernel takes this call (else the generic kernel).
+static bool fast_path(int64_t k, const void* x, const void* w, GemvShape* sh, int64_t n_out,
+                      int out_per_group) {
+  if (k % 64 != 0 || (uintptr_t)w % 4 != 0 || (uintptr_t)x % 16 != 0) return false;
+  const int ngroups = (int)((k / 64 + 7) / 8);
+  *sh = pick_shape((int)n_out, out_per_group, ngroups);
+  return sh->np <= 8;
+}
+
+// Grid size of the streaming kernel for an argmax GEMV (keys written).
+static int64_t argmax_workgroups(int64_t n, int64_t k, const void* x, const void* w) {
+  GemvShape sh;
+  if (!fast_path(k, x, w, &sh, n, 8)) return -1;
+  return (n + 8 * sh.rg - 1) / (8 * sh.rg);
+}
+
+static hipError_t gemv_dispatch(hipStream_t s, GemvArgs a, int64_t k, int epi, bool pro) {
+  const int64_t nblocks = k / 32;
+  a.npairs = (int)(nblocks / 2);
+  GemvShape sh{1, 1, 1};
+  if (!fast_path(k, a.x, a.w, &sh, a.n_out, epi == EPI_SWIGLU ? 4 : 8)) {
+    if (pro || epi == EPI_ARGMAX) return hipErrorInvalidValue;  // callers check first
+    if (epi == EPI_SWIGLU)
+      hipLaunchKernelGGL(q4_0_gemv_generic_kernel<true>, dim3((unsigned)a.n_out), dim3(64), 0, s,
+                         a.x, a.w, a.y, a.n_out, (int)nblocks, a.up_offset_rows);
     else
-      hipLaunchKernelGGL(q4_0_gemv_generic_kernel<false>, dim3((unsigned)n_out), dim3(64), 0, s,
-                         (const uint16_t*)x, (const uint8_t*)w, (uint16_t*)y, (int)n_out,
-                         (int)nblocks, up_rows);
+      hipLaunchKernelGGL(q4_0_gemv_generic_kernel<false>, dim3((unsigned)a.n_out), dim3(64), 0,
+                         s, a.x, a.w, a.y, a.n_out, (int)nblocks, a.up_offset_rows);
     return hipGetLastError();
   }
-#define SMX_NP_CASE(NPV)                                                                      \
-  case NPV:                                                                                   \
-    return swiglu ? dispatch_rg<NPV, true>(s, x, w, y, (int)n_out, npairs, up_rows, sh)       \
-                  : dispatch_rg<NPV, false>(s, x, w, y, (int)n_out, npairs, up_rows, sh);
-  switch (sh.np) {
-    SMX_NP_CASE(1)
-    SMX_NP_CASE(2)
-    SMX_NP_CASE(3)
-    SMX_NP_CASE(4)
-    SMX_NP_CASE(5)
-    SMX_NP_CASE(6)
-    SMX_NP_CASE(7)
-    SMX_NP_CASE(8)
-    default:
-      return hipErrorInvalidValue;
+  if (pro) {
+    if (epi == EPI_SWIGLU) return dispatch_np<true, EPI_SWIGLU>(s, a, sh);
+    if (epi == EPI_ARGMAX) return dispatch_np<true, EPI_ARGMAX>(s, a, sh);
+    return dispatch_np<true, EPI_STORE>(s, a, sh);
   }
-#undef SMX_NP_CASE
+  if (epi == EPI_SWIGLU) return dispatch_np<false, EPI_SWIGLU>(s, a, sh);
+  if (epi == EPI_ARGMAX) return dispatch_np<false, EPI_ARGMAX>(s, a, sh);
+  return dispatch_np<false, EPI_STORE>(s, a, sh);
 }
 
 }  // namespace smx
@@ -395,6 +494,15 @@ extern "C" int smx_q4_0_dequant_bf16(void* stream, const void* w, void* out, int
   return (int)hipGetLastError();
 }
 
+static smx::GemvArgs plain_args(const void* x, const void* w, void* y, int64_t n) {
+  smx::GemvArgs a{};
+  a.x = (const uint16_t*)x;
+  a.w = (const uint8_t*)w;
+  a.y = (uint16_t*)y;
+  a.n_out = (int)n;
+  return a;
+}
+
 extern "C" int smx_q4_0_gemv(void* stream, const void* x, const void* w, void* y, int64_t n,
                              int64_t k) {
   SMX_REQUIRE(x && w && y, "x, w and y must be non-null");
@@ -402,7 +510,8 @@ extern "C" int smx_q4_0_gemv(void* stream, const void* x, const void* w, void* y
   SMX_REQUIRE(k >= 32 && k % 32 == 0 && k <= (1 << 20), "k must be a multiple of 32 in [32, 2^20]");
   SMX_REQUIRE((uintptr_t)x % 2 == 0 && (uintptr_t)w % 2 == 0 && (uintptr_t)y % 2 == 0,
               "x, w and y must be 2-byte aligned");
-  return (int)smx::gemv_dispatch((hipStream_t)stream, x, w, y, n, k, false);
+  return (int)smx::gemv_dispatch((hipStream_t)stream, plain_args(x, w, y, n), k, smx::EPI_STORE,
+                                 false);
 }
 
 extern "C" int smx_q4_0_gemv_swiglu(void* stream, const void* x, const void* w, void* out,
@@ -412,5 +521,75 @@ extern "C" int smx_q4_0_gemv_swiglu(void* stream, const void* x, const void* w, 
   SMX_REQUIRE(k >= 32 && k % 32 == 0 && k <= (1 << 20), "k must be a multiple of 32 in [32, 2^20]");
   SMX_REQUIRE((uintptr_t)x % 2 == 0 && (uintptr_t)w % 2 == 0 && (uintptr_t)out % 2 == 0,
               "x, w and out must be 2-byte aligned");
-  return (int)smx::gemv_dispatch((hipStream_t)stream, x, w, out, d, k, true);
+  smx::GemvArgs a = plain_args(x, w, out, d);
+  a.up_offset_rows = d;
+  return (int)smx::gemv_dispatch((hipStream_t)stream, a, k, smx::EPI_SWIGLU, false);
+}
+
+// Shared checks of the entries with the add+RMSNorm prologue.
+#define SMX_NORM_GEMV_CHECKS(X, W, OUT, N)                                                       \
+  SMX_REQUIRE(X && gamma && W && OUT, "x, gamma, w and the output must be non-null");           \
+  SMX_REQUIRE(N >= 1 && N < (1ll << 30), "output size out of range");                           \
+  SMX_REQUIRE(k >= 64 && k % 64 == 0 && k <= 65536, "k must be a multiple of 64 in [64, 65536]"); \
+  SMX_REQUIRE(eps >= 0.f && std::isfinite(eps), "eps must be finite and >= 0");                 \
+  SMX_REQUIRE((uintptr_t)X % 16 == 0 && (uintptr_t)gamma % 16 == 0 &&                            \
+                  (uintptr_t)residual % 16 == 0 && (uintptr_t)residual_out % 16 == 0 &&         \
+                  (uintptr_t)W % 4 == 0 && (uintptr_t)OUT % 2 == 0,                              \
+              "x, residual, gamma, residual_out 16-byte aligned; w 4-byte aligned");             \
+  SMX_REQUIRE(!residual_out || (residual_out != residual && residual_out != X),                  \
+              "residual_out must not alias x or residual");                                      \
+  {                                                                                              \
+    smx::GemvShape sh_;                                                                          \
+    SMX_REQUIRE(smx::fast_path(k, X, W, &sh_, N, 8), "shape not supported by the fused kernel");  \
+  }
+
+static smx::GemvArgs norm_args(const void* x, const void* residual, const void* gamma,
+                               void* residual_out, const void* w, void* y, int64_t n,
+                               float eps) {
+  smx::GemvArgs a = plain_args(x, w, y, n);
+  a.residual = (const uint16_t*)residual;
+  a.gamma = (const uint16_t*)gamma;
+  a.residual_out = (uint16_t*)residual_out;
+  a.eps = eps;
+  return a;
+}
+
+extern "C" int smx_q4_0_add_rmsnorm_gemv(void* stream, const void* x, const void* residual,
+                                         const void* gamma, void* residual_out, const void* w,
+                                         void* y, int64_t n, int64_t k, float eps) {
+  SMX_NORM_GEMV_CHECKS(x, w, y, n);
+  return (int)smx::gemv_dispatch(
+      (hipStream_t)stream, norm_args(x, residual, gamma, residual_out, w, y, n, eps), k,
+      smx::EPI_STORE, true);
+}
+
+extern "C" int smx_q4_0_add_rmsnorm_gemv_swiglu(void* stream, const void* x, const void* residual,
+                                                const void* gamma, void* residual_out,
+                                                const void* w, void* out, int64_t d, int64_t k,
+                                                float eps) {
+  SMX_NORM_GEMV_CHECKS(x, w, out, d);
+  smx::GemvArgs a = norm_args(x, residual, gamma, residual_out, w, out, d, eps);
+  a.up_offset_rows = d;
+  return (int)smx::gemv_dispatch((hipStream_t)stream, a, k, smx::EPI_SWIGLU, true);
+}
+
+extern "C" int64_t smx_q4_0_argmax_keys_size(int64_t n, int64_t k) {
+  if (n < 1 || k < 64 || k % 64) return -1;
+  static const uint16_t dummy[8] __attribute__((aligned(16))) = {};
+  return smx::argmax_workgroups(n, k, dummy, dummy);
+}
+
+extern "C" int smx_q4_0_add_rmsnorm_gemv_argmax(void* stream, const void* x,
+                                                const void* residual, const void* gamma,
+                                                const void* w, void* logits, uint64_t* keys,
+                                                int64_t num_keys, int64_t n, int64_t k,
+                                                float eps) {
+  void* residual_out = nullptr;
+  SMX_NORM_GEMV_CHECKS(x, w, logits, n);
+  SMX_REQUIRE(keys && (uintptr_t)keys % 8 == 0, "keys must be non-null and 8-byte aligned");
+  SMX_REQUIRE(num_keys == smx::argmax_workgroups(n, k, x, w),
+              "num_keys must equal smx_q4_0_argmax_keys_size(n, k)");
+  smx::GemvArgs a = norm_args(x, residual, gamma, nullptr, w, logits, n, eps);
+  a.argmax_keys = keys;
+  return (int)smx::gemv_dispatch((hipStream_t)stream, a, k, smx::EPI_ARGMAX, true);
 }

@@ -205,15 +205,34 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const uint16_t* __restrict
   }
 }
 
-__global__ void decode_advance_kernel(const int64_t* __restrict__ next_ids,
-                                      const int64_t* __restrict__ forced_ids,
-                                      const int32_t* __restrict__ forced_len,
-                                      int64_t* ids, int64_t* positions, int32_t* seq_lens,
-                                      int64_t* slot_mapping, const int32_t* block_table,
-                                      int64_t* tokens_out, int rows, int max_blocks,
-                                      int block_size, int max_len) {
-  const int r = blockIdx.x * blockDim.x + threadIdx.x;
-  if (r >= rows) return;
+// One workgroup of 1024 threads per row.  With argmax_keys, the row's next
+// token is first reduced from the per-workgroup keys of the head GEMV
+// (max value, then lowest index) and stored to next_ids.
+__global__ __launch_bounds__(1024) void decode_advance_kernel(
+    int64_t* __restrict__ next_ids, const uint64_t* __restrict__ argmax_keys, int num_keys,
+    const int64_t* __restrict__ forced_ids, const int32_t* __restrict__ forced_len,
+    int64_t* ids, int64_t* positions, int32_t* seq_lens, int64_t* slot_mapping,
+    const int32_t* block_table, int64_t* tokens_out, int max_blocks, int block_size,
+    int max_len) {
+  __shared__ uint64_t red[16];
+  const int r = blockIdx.x;
+  if (argmax_keys) {
+    uint64_t key = 0;
+    const uint64_t* kr = argmax_keys + (int64_t)r * num_keys;
+    for (int i = threadIdx.x; i < num_keys; i += blockDim.x) key = kr[i] > key ? kr[i] : key;
+    for (int m = 1; m < 64; m <<= 1) {
+      const uint64_t o = ((uint64_t)(uint32_t)__shfl_xor((int)(key >> 32), m, 64) << 32) |
+                         (uint32_t)__shfl_xor((int)(uint32_t)key, m, 64);
+      key = o > key ? o : key;
+    }
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = key;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      for (int i = 1; i < (int)(blockDim.x >> 6); ++i) key = red[i] > key ? red[i] : key;
+      next_ids[r] = key ? (int64_t)(0xffffffffu - (uint32_t)key) : 0;
+    }
+  }
+  if (threadIdx.x != 0) return;
   const int64_t p = positions[r] + 1;
   const int64_t nid = (forced_ids && p < forced_len[r] && p < max_len)
                           ? forced_ids[(int64_t)r * max_len + p]
@@ -344,20 +363,24 @@ extern "C" int smx_reshape_and_cache(void* stream, const void* key, const void* 
   return (int)hipGetLastError();
 }
 
-extern "C" int smx_decode_advance(void* stream, const int64_t* next_ids,
-                                  const int64_t* forced_ids, const int32_t* forced_len, int64_t* ids,
-                                  int64_t* positions, int32_t* seq_lens, int64_t* slot_mapping,
+extern "C" int smx_decode_advance(void* stream, int64_t* next_ids, const uint64_t* argmax_keys,
+                                  int32_t num_keys, const int64_t* forced_ids,
+                                  const int32_t* forced_len, int64_t* ids, int64_t* positions,
+                                  int32_t* seq_lens, int64_t* slot_mapping,
                                   const int32_t* block_table, int64_t* tokens_out, int32_t rows,
                                   int32_t max_blocks, int32_t block_size, int32_t max_len) {
   SMX_REQUIRE(next_ids && ids && positions && seq_lens && slot_mapping && block_table,
               "null pointer argument");
-  SMX_REQUIRE(rows >= 1 && max_blocks >= 1 && block_size >= 1 && max_len >= 0, "bad sizes");
+  SMX_REQUIRE(rows >= 1 && rows <= 65535 && max_blocks >= 1 && block_size >= 1 && max_len >= 0,
+              "bad sizes");
   SMX_REQUIRE((forced_ids == nullptr) == (forced_len == nullptr),
               "forced_ids and forced_len go together");
   SMX_REQUIRE(!forced_ids || max_len >= 1, "forced_ids needs max_len >= 1");
-  hipLaunchKernelGGL(smx::decode_advance_kernel, dim3((rows + 63) / 64), dim3(64), 0,
-                     (hipStream_t)stream, next_ids, forced_ids, forced_len, ids, positions,
-                     seq_lens, slot_mapping, block_table, tokens_out, rows, max_blocks,
+  SMX_REQUIRE(!argmax_keys || num_keys >= 1, "argmax_keys needs num_keys >= 1");
+  SMX_REQUIRE((uintptr_t)argmax_keys % 8 == 0, "argmax_keys must be 8-byte aligned");
+  hipLaunchKernelGGL(smx::decode_advance_kernel, dim3(rows), dim3(argmax_keys ? 1024 : 64), 0,
+                     (hipStream_t)stream, next_ids, argmax_keys, num_keys, forced_ids, forced_len,
+                     ids, positions, seq_lens, slot_mapping, block_table, tokens_out, max_blocks,
                      block_size, max_len);
   return (int)hipGetLastError();
 }

@@ -64,13 +64,51 @@ constexpr int BLK = 64;  // tokens per wave block: all K and V loads of a block 
 //  PV: 16 lanes per token, 8 dims each; two tokens' V are spliced into bf16
 //      pairs (v_perm_b32) that meet the bf16 probability pairs, staged in
 //      LDS, in v_dot2c_f32_bf16.
-template <int WAVES>
-__global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
-    const uint16_t* __restrict__ vc, const int32_t* __restrict__ block_table,
-    const int32_t* __restrict__ seq_lens, float* __restrict__ part_o,
-    float* __restrict__ part_lse, int num_splits, int max_blocks, int num_blocks, int bs_log2,
-    int n_q, int n_kv, float scale_log2) {
+struct SplitKVArgs {
+  const uint16_t* q;  // [num_seqs, n_q, HD] (plain) or the raw QKV row (FUSEQ)
+  const uint16_t* kc;
+  uint16_t* vc_w;     // v cache (written by FUSEQ)
+  uint16_t* kc_w;     // k cache (written by FUSEQ)
+  const uint16_t* vc;
+  const int32_t* block_table;
+  const int32_t* seq_lens;
+  float* part_o;
+  float* part_lse;
+  // FUSEQ only
+  const uint16_t* q_gamma;
+  const uint16_t* k_gamma;
+  const uint16_t* cos_sin;
+  const int64_t* positions;
+  const int64_t* slot_mapping;
+  int max_position;
+  float eps;
+  int num_splits, max_blocks, num_blocks, bs_log2, n_q, n_kv;
+  float scale_log2;
+};
+
+// RMSNorm (gamma) + neox RoPE of one 128-wide head held by a wave as
+// (a, b) = dims (lane, lane + 64); returns the rotated pair as bf16 bits.
+__device__ __forceinline__ void norm_rope_head(float a, float b, const uint16_t* gamma, float c,
+                                               float sn, float eps, int lane, uint16_t* u_out,
+                                               uint16_t* v_out) {
+  const float ss = wave_sum(a * a + b * b);
+  const float inv = 1.0f / sqrtf(ss / (float)HD + eps);
+  const float an = round_bf16(a * inv * bf16_bits_to_f32(gamma[lane]));
+  const float bn = round_bf16(b * inv * bf16_bits_to_f32(gamma[lane + 64]));
+  *u_out = f32_to_bf16(an * c - bn * sn);
+  *v_out = f32_to_bf16(bn * c + an * sn);
+}
+
+template <int WAVES, bool FUSEQ>
+__global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(SplitKVArgs A) {
+  const uint16_t* __restrict__ kc = A.kc;
+  const uint16_t* __restrict__ vc = A.vc;
+  const int32_t* __restrict__ block_table = A.block_table;
+  float* __restrict__ part_o = A.part_o;
+  float* __restrict__ part_lse = A.part_lse;
+  const int num_splits = A.num_splits, max_blocks = A.max_blocks, num_blocks = A.num_blocks;
+  const int bs_log2 = A.bs_log2, n_q = A.n_q, n_kv = A.n_kv;
+  const float scale_log2 = A.scale_log2;
   constexpr int NT = 64 * WAVES;
   __shared__ __attribute__((aligned(16))) uint32_t q_lds[G * HD / 2];  // 4 heads, bf16 pairs
   __shared__ __attribute__((aligned(16))) uint32_t p2[WAVES][128];     // [jp 8][vt 4][h 4]
@@ -92,10 +130,50 @@ __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(
   const int32_t* bt = block_table + (int64_t)seq * max_blocks;
   const int bt0 = bt[w0 < cap ? (w0 >> bs_log2) : 0];
   const int bt1 = bt[w0 + 32 < cap ? ((w0 + 32) >> bs_log2) : 0];
-  const int L = min(seq_lens[seq], cap);
-  if (tid < G * HD / 8)
-    reinterpret_cast<u32x4*>(q_lds)[tid] =
-        reinterpret_cast<const u32x4*>(q + ((int64_t)seq * n_q + kvh * G) * HD)[tid];
+  const int L = min(A.seq_lens[seq], cap);
+  // The new token (FUSEQ): its K/V are produced here by the workgroup whose
+  // split holds its position.
+  __shared__ __attribute__((aligned(16))) uint32_t kv_new[2][HD / 2];
+  int64_t pos = 0;
+  bool owner = false;
+  if constexpr (FUSEQ) {
+    pos = A.positions[seq];
+    owner = pos >= s0 && pos < s0 + tps && pos < L;
+    const int nh = n_q + 2 * n_kv;
+    const uint16_t* row = A.q + (int64_t)seq * nh * HD;
+    const int64_t pc = pos < 0 ? 0 : (pos >= A.max_position ? A.max_position - 1 : pos);
+    const float c = bf16_bits_to_f32(A.cos_sin[pc * HD + lane]);
+    const float sn = bf16_bits_to_f32(A.cos_sin[pc * HD + 64 + lane]);
+    uint16_t* qh = reinterpret_cast<uint16_t*>(q_lds);
+    for (int h = wave; h < G; h += WAVES) {
+      const uint16_t* src = row + (kvh * G + h) * HD;
+      norm_rope_head(bf16_bits_to_f32(src[lane]), bf16_bits_to_f32(src[lane + 64]), A.q_gamma,
+                     c, sn, A.eps, lane, &qh[h * HD + lane], &qh[h * HD + 64 + lane]);
+    }
+    if (owner && wave == (G % WAVES)) {
+      const uint16_t* ksrc = row + (n_q + kvh) * HD;
+      const uint16_t* vsrc = row + (n_q + n_kv + kvh) * HD;
+      uint16_t* kn = reinterpret_cast<uint16_t*>(kv_new[0]);
+      uint16_t* vn = reinterpret_cast<uint16_t*>(kv_new[1]);
+      norm_rope_head(bf16_bits_to_f32(ksrc[lane]), bf16_bits_to_f32(ksrc[lane + 64]), A.k_gamma,
+                     c, sn, A.eps, lane, &kn[lane], &kn[lane + 64]);
+      vn[lane] = vsrc[lane];
+      vn[lane + 64] = vsrc[lane + 64];
+      const int64_t slot = A.slot_mapping[seq];
+      if (slot >= 0 && slot < ((int64_t)num_blocks << bs_log2)) {
+        uint16_t* kd = A.kc_w + (slot * n_kv + kvh) * HD;
+        uint16_t* vd = A.vc_w + (slot * n_kv + kvh) * HD;
+        kd[lane] = kn[lane];
+        kd[lane + 64] = kn[lane + 64];
+        vd[lane] = vsrc[lane];
+        vd[lane + 64] = vsrc[lane + 64];
+      }
+    }
+  } else {
+    if (tid < G * HD / 8)
+      reinterpret_cast<u32x4*>(q_lds)[tid] =
+          reinterpret_cast<const u32x4*>(A.q + ((int64_t)seq * n_q + kvh * G) * HD)[tid];
+  }
   const int s1 = min(L, s0 + tps);
   float* po = part_o + (((int64_t)seq * num_splits + split) * n_q + kvh * G) * HD;
   float* pl = part_lse + ((int64_t)seq * num_splits + split) * n_q + kvh * G;
@@ -166,6 +244,24 @@ __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(
       for (int hf = 0; hf < 2; ++hf)
         vr[jp][hf] = reinterpret_cast<const u32x4*>(vc + tok_off(8 * jp + vt + 4 * hf))[dv];
 
+    if constexpr (FUSEQ) {
+      // The new token's K/V come from LDS (its cache slot is written by this
+      // same launch, which does not order the store before these loads).
+      const int tp = (int)(pos - t0);
+      if (owner && tp >= 0 && tp < BLK) {
+#pragma unroll
+        for (int r = 0; r < 8; ++r)
+          if (8 * r + tok == tp) {
+            kr[r][0] = reinterpret_cast<const u32x4*>(kv_new[0])[dq];
+            kr[r][1] = reinterpret_cast<const u32x4*>(kv_new[0])[dq + 8];
+          }
+#pragma unroll
+        for (int jp = 0; jp < 8; ++jp)
+#pragma unroll
+          for (int hf = 0; hf < 2; ++hf)
+            if (8 * jp + vt + 4 * hf == tp) vr[jp][hf] = reinterpret_cast<const u32x4*>(kv_new[1])[dv];
+      }
+    }
     // ---- scores: token 8r + tok, head hsel
     float sm[8];
 #pragma unroll
@@ -361,32 +457,52 @@ __global__ __launch_bounds__(256) void lse_merge_kernel(const float* __restrict_
 #include "smx_abi_util.h"
 
 namespace {
-int launch_splitkv(void* stream, const void* q, const void* k_cache, const void* v_cache,
-                   const int32_t* block_table, const int32_t* seq_lens, float* partial_o,
-                   float* partial_lse, int32_t num_seqs, int32_t num_splits, int32_t max_blocks,
-                   int32_t num_blocks, int32_t block_size, int32_t n_q, int32_t n_kv,
+template <bool FUSEQ>
+int launch_splitkv(void* stream, smx::SplitKVArgs a, int32_t num_seqs, int32_t block_size,
                    float scale) {
   int bs_log2 = 0;
   while ((1 << bs_log2) < block_size) ++bs_log2;
-  const float scale_log2 = scale * 1.44269504088896340736f;
+  a.bs_log2 = bs_log2;
+  a.scale_log2 = scale * 1.44269504088896340736f;
   // One 64-token block per wave: the wave count follows the split size.
-  const int64_t cap = (int64_t)max_blocks * block_size;
-  const int64_t tps = ((cap + num_splits - 1) / num_splits + 31) / 32 * 32;
+  const int64_t cap = (int64_t)a.max_blocks * block_size;
+  const int64_t tps = ((cap + a.num_splits - 1) / a.num_splits + 31) / 32 * 32;
   int waves = tps <= 64 ? 1 : tps <= 128 ? 2 : tps <= 256 ? 4 : 8;
   const char* e = getenv("SMX_ATTN_WAVES");  // override for tuning sweeps
   if (e && (atoi(e) == 1 || atoi(e) == 2 || atoi(e) == 4 || atoi(e) == 8)) waves = atoi(e);
-  const dim3 grid(num_splits, n_kv, num_seqs);
-#define SMX_ATTN_LAUNCH(W)                                                                   \
-  hipLaunchKernelGGL(smx::splitkv_decode_kernel<W>, grid, dim3(64 * W), 0, (hipStream_t)stream, \
-                     (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache,  \
-                     block_table, seq_lens, partial_o, partial_lse, num_splits, max_blocks,   \
-                     num_blocks, bs_log2, n_q, n_kv, scale_log2)
+  const dim3 grid(a.num_splits, a.n_kv, num_seqs);
+#define SMX_ATTN_LAUNCH(W)                                                                      \
+  hipLaunchKernelGGL((smx::splitkv_decode_kernel<W, FUSEQ>), grid, dim3(64 * W), 0,             \
+                     (hipStream_t)stream, a)
   if (waves == 8) SMX_ATTN_LAUNCH(8);
   else if (waves == 4) SMX_ATTN_LAUNCH(4);
   else if (waves == 2) SMX_ATTN_LAUNCH(2);
   else SMX_ATTN_LAUNCH(1);
 #undef SMX_ATTN_LAUNCH
   return (int)hipGetLastError();
+}
+
+smx::SplitKVArgs splitkv_args(const void* q, const void* k_cache, const void* v_cache,
+                              const int32_t* block_table, const int32_t* seq_lens,
+                              float* partial_o, float* partial_lse, int32_t num_splits,
+                              int32_t max_blocks, int32_t num_blocks, int32_t n_q,
+                              int32_t n_kv) {
+  smx::SplitKVArgs a{};
+  a.q = (const uint16_t*)q;
+  a.kc = (const uint16_t*)k_cache;
+  a.vc = (const uint16_t*)v_cache;
+  a.kc_w = (uint16_t*)k_cache;
+  a.vc_w = (uint16_t*)v_cache;
+  a.block_table = block_table;
+  a.seq_lens = seq_lens;
+  a.part_o = partial_o;
+  a.part_lse = partial_lse;
+  a.num_splits = num_splits;
+  a.max_blocks = max_blocks;
+  a.num_blocks = num_blocks;
+  a.n_q = n_q;
+  a.n_kv = n_kv;
+  return a;
 }
 
 int launch_merge(void* stream, const float* partial_o, const float* partial_lse, void* out,
@@ -422,9 +538,11 @@ extern "C" int smx_splitkv_decode(void* stream, const void* q, const void* k_cac
                                   int32_t num_blocks, int32_t block_size, int32_t n_q,
                                   int32_t n_kv, int32_t head_dim, float scale) {
   SMX_SPLITKV_CHECKS();
-  return launch_splitkv(stream, q, k_cache, v_cache, block_table, seq_lens, partial_o,
-                        partial_lse, num_seqs, num_splits, max_blocks, num_blocks, block_size, n_q,
-                        n_kv, scale);
+  return launch_splitkv<false>(stream,
+                               splitkv_args(q, k_cache, v_cache, block_table, seq_lens,
+                                            partial_o, partial_lse, num_splits, max_blocks,
+                                            num_blocks, n_q, n_kv),
+                               num_seqs, block_size, scale);
 }
 
 extern "C" int smx_splitkv_decode_merged(void* stream, const void* q, const void* k_cache,
@@ -436,9 +554,42 @@ extern "C" int smx_splitkv_decode_merged(void* stream, const void* q, const void
                                          int32_t n_kv, int32_t head_dim, float scale) {
   SMX_SPLITKV_CHECKS();
   SMX_REQUIRE(out && (uintptr_t)out % 2 == 0, "out must be non-null and 2-byte aligned");
-  const int rc = launch_splitkv(stream, q, k_cache, v_cache, block_table, seq_lens, partial_o,
-                                partial_lse, num_seqs, num_splits, max_blocks, num_blocks,
-                                block_size, n_q, n_kv, scale);
+  const int rc = launch_splitkv<false>(stream,
+                                       splitkv_args(q, k_cache, v_cache, block_table, seq_lens,
+                                                    partial_o, partial_lse, num_splits,
+                                                    max_blocks, num_blocks, n_q, n_kv),
+                                       num_seqs, block_size, scale);
+  if (rc) return rc;
+  return launch_merge(stream, partial_o, partial_lse, out, num_seqs, num_splits, n_q);
+}
+
+extern "C" int smx_qknorm_rope_splitkv_decode_merged(
+    void* stream, const void* qkv, const void* q_gamma, const void* k_gamma,
+    const void* cos_sin, const int64_t* positions, const int64_t* slot_mapping, void* k_cache,
+    void* v_cache, const int32_t* block_table, const int32_t* seq_lens, float* partial_o,
+    float* partial_lse, void* out, int32_t num_seqs, int32_t num_splits, int32_t max_blocks,
+    int32_t num_blocks, int32_t block_size, int32_t n_q, int32_t n_kv, int32_t head_dim,
+    int32_t max_position, float eps, float scale) {
+  const void* q = qkv;
+  SMX_SPLITKV_CHECKS();
+  SMX_REQUIRE(q_gamma && k_gamma && cos_sin && positions && slot_mapping && out,
+              "null pointer argument");
+  SMX_REQUIRE(max_position >= 1, "max_position must be >= 1");
+  SMX_REQUIRE(eps >= 0.f && isfinite(eps), "eps must be finite and >= 0");
+  SMX_REQUIRE((uintptr_t)positions % 8 == 0 && (uintptr_t)slot_mapping % 8 == 0 &&
+                  (uintptr_t)out % 2 == 0 && (uintptr_t)q_gamma % 2 == 0 &&
+                  (uintptr_t)k_gamma % 2 == 0 && (uintptr_t)cos_sin % 2 == 0,
+              "misaligned pointer");
+  smx::SplitKVArgs a = splitkv_args(qkv, k_cache, v_cache, block_table, seq_lens, partial_o,
+                                    partial_lse, num_splits, max_blocks, num_blocks, n_q, n_kv);
+  a.q_gamma = (const uint16_t*)q_gamma;
+  a.k_gamma = (const uint16_t*)k_gamma;
+  a.cos_sin = (const uint16_t*)cos_sin;
+  a.positions = positions;
+  a.slot_mapping = slot_mapping;
+  a.max_position = max_position;
+  a.eps = eps;
+  const int rc = launch_splitkv<true>(stream, a, num_seqs, block_size, scale);
   if (rc) return rc;
   return launch_merge(stream, partial_o, partial_lse, out, num_seqs, num_splits, n_q);
 }

@@ -254,9 +254,12 @@ def decode_advance(next_ids: torch.Tensor, ids: torch.Tensor, positions: torch.T
                    seq_lens: torch.Tensor, slot_mapping: torch.Tensor, block_table: torch.Tensor,
                    block_size: int, tokens_out: torch.Tensor | None = None,
                    forced_ids: torch.Tensor | None = None,
-                   forced_len: torch.Tensor | None = None) -> None:
+                   forced_len: torch.Tensor | None = None,
+                   argmax_keys: torch.Tensor | None = None) -> None:
     """forced_ids [rows, max_len] int64 with forced_len [rows] int32 on the
-    device; tokens_out [rows, max_len] int64 (same max_len)."""
+    device; tokens_out [rows, max_len] int64 (same max_len); argmax_keys
+    [rows, num_keys] int64 from add_rmsnorm_gemv_argmax (next_ids is then
+    written with the argmax)."""
     rows = ids.numel()
     _check(next_ids, "next_ids", torch.int64, rows)
     _check(ids, "ids", torch.int64, rows, next_ids.device)
@@ -275,9 +278,121 @@ def decode_advance(next_ids: torch.Tensor, ids: torch.Tensor, positions: torch.T
             max_len = t.shape[1]
     if forced_len is not None:
         _check(forced_len, "forced_len", torch.int32, rows, next_ids.device)
+    num_keys = 0
+    if argmax_keys is not None:
+        _check(argmax_keys, "argmax_keys", torch.int64, device=next_ids.device)
+        _need(argmax_keys.dim() == 2 and argmax_keys.shape[0] == rows, "argmax_keys must be [rows, n]")
+        num_keys = argmax_keys.shape[1]
     call("smx_decode_advance", _stream(ids), next_ids.data_ptr(),
+         argmax_keys.data_ptr() if argmax_keys is not None else None, num_keys,
          forced_ids.data_ptr() if forced_ids is not None else None,
          forced_len.data_ptr() if forced_len is not None else None, ids.data_ptr(),
          positions.data_ptr(), seq_lens.data_ptr(), slot_mapping.data_ptr(), block_table.data_ptr(),
          tokens_out.data_ptr() if tokens_out is not None else None, rows, block_table.shape[1],
          block_size, max_len)
+
+
+def _norm_gemv_checks(x, residual, gamma, residual_out, k):
+    _check(x, "x", BF16, k)
+    _check(gamma, "gamma", BF16, k, x.device)
+    if residual is not None:
+        _check(residual, "residual", BF16, k, x.device)
+    if residual_out is not None:
+        _check(residual_out, "residual_out", BF16, k, x.device)
+        _need(residual_out.data_ptr() not in (x.data_ptr(),
+                                               residual.data_ptr() if residual is not None else -1),
+              "residual_out must not alias x or residual")
+
+
+def _ptr(t):
+    return t.data_ptr() if t is not None else None
+
+
+def add_rmsnorm_gemv(x: torch.Tensor, residual: torch.Tensor | None, gamma: torch.Tensor,
+                     w: torch.Tensor, n: int, k: int, eps: float,
+                     residual_out: torch.Tensor | None = None,
+                     out: torch.Tensor | None = None) -> torch.Tensor:
+    """y = W . (RMSNorm(x + residual) * gamma); residual_out = bf16(x + residual)."""
+    _norm_gemv_checks(x, residual, gamma, residual_out, k)
+    _check(w, "w", torch.uint8, n * q4_0_row_bytes(k), x.device)
+    if out is None:
+        out = torch.empty((1, n), dtype=BF16, device=x.device)
+    _check(out, "out", BF16, n, x.device)
+    call("smx_q4_0_add_rmsnorm_gemv", _stream(x), x.data_ptr(), _ptr(residual), gamma.data_ptr(),
+         _ptr(residual_out), w.data_ptr(), out.data_ptr(), n, k, float(eps))
+    return out
+
+
+def add_rmsnorm_gemv_swiglu(x: torch.Tensor, residual: torch.Tensor | None, gamma: torch.Tensor,
+                            w: torch.Tensor, d: int, k: int, eps: float,
+                            residual_out: torch.Tensor | None = None,
+                            out: torch.Tensor | None = None) -> torch.Tensor:
+    _norm_gemv_checks(x, residual, gamma, residual_out, k)
+    _check(w, "w", torch.uint8, 2 * d * q4_0_row_bytes(k), x.device)
+    if out is None:
+        out = torch.empty((1, d), dtype=BF16, device=x.device)
+    _check(out, "out", BF16, d, x.device)
+    call("smx_q4_0_add_rmsnorm_gemv_swiglu", _stream(x), x.data_ptr(), _ptr(residual),
+         gamma.data_ptr(), _ptr(residual_out), w.data_ptr(), out.data_ptr(), d, k, float(eps))
+    return out
+
+
+def argmax_keys_size(n: int, k: int) -> int:
+    from . import load
+    return int(load().smx_q4_0_argmax_keys_size(n, k))
+
+
+def add_rmsnorm_gemv_argmax(x: torch.Tensor, residual: torch.Tensor | None, gamma: torch.Tensor,
+                            w: torch.Tensor, n: int, k: int, eps: float, keys: torch.Tensor,
+                            out: torch.Tensor | None = None) -> torch.Tensor:
+    """Logits = W . RMSNorm(x + residual) * gamma, plus per-workgroup argmax
+    keys [argmax_keys_size(n, k)] int64 for decode_advance."""
+    _norm_gemv_checks(x, residual, gamma, None, k)
+    _check(w, "w", torch.uint8, n * q4_0_row_bytes(k), x.device)
+    _check(keys, "keys", torch.int64, device=x.device)
+    if out is None:
+        out = torch.empty((1, n), dtype=BF16, device=x.device)
+    _check(out, "out", BF16, n, x.device)
+    call("smx_q4_0_add_rmsnorm_gemv_argmax", _stream(x), x.data_ptr(), _ptr(residual),
+         gamma.data_ptr(), w.data_ptr(), out.data_ptr(), keys.data_ptr(), keys.numel(), n, k,
+         float(eps))
+    return out
+
+
+def qknorm_rope_splitkv_decode_merged(qkv: torch.Tensor, q_gamma: torch.Tensor,
+                                      k_gamma: torch.Tensor, cos_sin: torch.Tensor,
+                                      positions: torch.Tensor, slot_mapping: torch.Tensor,
+                                      k_cache: torch.Tensor, v_cache: torch.Tensor,
+                                      block_table: torch.Tensor, seq_lens: torch.Tensor,
+                                      num_splits: int, scale: float, eps: float, n_q: int,
+                                      partial_o: torch.Tensor, partial_lse: torch.Tensor,
+                                      out: torch.Tensor | None = None) -> torch.Tensor:
+    """q/k RMSNorm + RoPE + KV write + split-KV decode + merge for one decode
+    token per sequence (qkv: raw QKV projection [num_seqs, (n_q+2n_kv)*hd])."""
+    num_blocks, bs, n_kv, hd = k_cache.shape
+    num_seqs = seq_lens.numel()
+    _check(qkv, "qkv", BF16, num_seqs * (n_q + 2 * n_kv) * hd)
+    _check(q_gamma, "q_gamma", BF16, hd, qkv.device)
+    _check(k_gamma, "k_gamma", BF16, hd, qkv.device)
+    _check(cos_sin, "cos_sin", BF16, device=qkv.device)
+    _need(cos_sin.dim() == 2 and cos_sin.shape[1] == hd, "cos_sin must be [max_position, head_dim]")
+    _check(positions, "positions", torch.int64, num_seqs, qkv.device)
+    _check(slot_mapping, "slot_mapping", torch.int64, num_seqs, qkv.device)
+    _check(k_cache, "k_cache", BF16, device=qkv.device)
+    _check(v_cache, "v_cache", BF16, device=qkv.device)
+    _need(tuple(v_cache.shape) == tuple(k_cache.shape), "k_cache and v_cache shapes differ")
+    _check(block_table, "block_table", torch.int32, device=qkv.device)
+    _need(block_table.dim() == 2 and block_table.shape[0] == num_seqs, "block_table must be [seqs, max_blocks]")
+    _check(seq_lens, "seq_lens", torch.int32, num_seqs, qkv.device)
+    _check(partial_o, "partial_o", torch.float32, num_seqs * num_splits * n_q * hd, qkv.device)
+    _check(partial_lse, "partial_lse", torch.float32, num_seqs * num_splits * n_q, qkv.device)
+    if out is None:
+        out = torch.empty((num_seqs, n_q, hd), dtype=BF16, device=qkv.device)
+    _check(out, "out", BF16, num_seqs * n_q * hd, qkv.device)
+    call("smx_qknorm_rope_splitkv_decode_merged", _stream(qkv), qkv.data_ptr(), q_gamma.data_ptr(),
+         k_gamma.data_ptr(), cos_sin.data_ptr(), positions.data_ptr(), slot_mapping.data_ptr(),
+         k_cache.data_ptr(), v_cache.data_ptr(), block_table.data_ptr(), seq_lens.data_ptr(),
+         partial_o.data_ptr(), partial_lse.data_ptr(), out.data_ptr(), num_seqs, num_splits,
+         block_table.shape[1], num_blocks, bs, n_q, n_kv, hd, cos_sin.shape[0], float(eps),
+         float(scale))
+    return out

@@ -62,10 +62,24 @@ def test_bindings_cover_header():
     ("smx_silu_mul", (None, 16, 16, 0, 10)),
     ("smx_embedding", (None, 16, 16, 16, 0, 10, 10)),
     ("smx_argmax_bf16", (None, 16, 0, 10, 16)),
-    ("smx_decode_advance", (None, 16, None, None, 16, 16, 16, 16, 16, None, 0, 1, 1, 0)),
-    ("smx_decode_advance", (None, 16, None, 16, 16, 16, 16, 16, 16, None, 1, 1, 1, 0)),
-    ("smx_decode_advance", (None, 16, 16, 16, 16, 16, 16, 16, 16, None, 1, 1, 1, 0)),
+    ("smx_decode_advance", (None, 16, None, 0, None, None, 16, 16, 16, 16, 16, None, 0, 1, 1, 0)),
+    ("smx_decode_advance", (None, 16, None, 0, None, 16, 16, 16, 16, 16, 16, None, 1, 1, 1, 0)),
+    ("smx_decode_advance", (None, 16, None, 0, 16, 16, 16, 16, 16, 16, 16, None, 1, 1, 1, 0)),
+    ("smx_decode_advance", (None, 16, 16, 0, None, None, 16, 16, 16, 16, 16, None, 1, 1, 1, 0)),
+    ("smx_q4_0_add_rmsnorm_gemv", (None, 16, 16, 16, 16, 16, 16, 64, 96, 1e-6)),
+    ("smx_q4_0_add_rmsnorm_gemv", (None, 16, 16, 16, 16, 16, 16, 64, 256, 1e-6)),
+    ("smx_q4_0_add_rmsnorm_gemv", (None, 16, 32, 16, 32, 16, 16, 64, 256, 1e-6)),
+    ("smx_q4_0_add_rmsnorm_gemv_swiglu", (None, 16, 32, 16, 64, 16, 16, 64, 2560, -1.0)),
+    ("smx_q4_0_add_rmsnorm_gemv_argmax", (None, 16, 32, 16, 16, 16, 16, 3, 64, 256, 1e-6)),
     ("smx_reshape_and_cache", (None, 16, 16, 16, 16, 16, 0, 8, 128, 4, 128)),
+    ("smx_qknorm_rope_splitkv_decode_merged",
+     (None, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16, 1, 4, 8, 8, 128, 32, 8, 128, 0, 1e-6, 0.1)),
+    ("smx_qknorm_rope_splitkv_decode_merged",
+     (None, 16, 16, 16, 16, 12, 16, 16, 16, 16, 16, 16, 16, 16, 1, 4, 8, 8, 128, 32, 8, 128, 100, 1e-6, 0.1)),
+    ("smx_qknorm_rope_splitkv_decode_merged",
+     (None, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16, None, 1, 4, 8, 8, 128, 32, 8, 128, 100, 1e-6, 0.1)),
+    ("smx_qknorm_rope_splitkv_decode_merged",
+     (None, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16, 1, 4, 8, 8, 128, 32, 8, 64, 100, 1e-6, 0.1)),
 ])
 def test_invalid_arguments_rejected_on_host(call, args):
     native = pkg("native")
@@ -73,6 +87,14 @@ def test_invalid_arguments_rejected_on_host(call, args):
     rc = getattr(lib, call)(*args)
     assert rc == native.SMX_EINVAL
     assert lib.smx_last_error().decode().startswith(call)
+
+
+def test_argmax_keys_size():
+    native = pkg("native")
+    lib = native.load()
+    assert lib.smx_q4_0_argmax_keys_size(151936, 2560) == 151936 // 16
+    assert lib.smx_q4_0_argmax_keys_size(1000, 256) == 125
+    assert lib.smx_q4_0_argmax_keys_size(1000, 96) == -1
 
 
 def test_call_raises_with_message():

@@ -13,6 +13,7 @@ import numpy as np
 import pytest
 
 from oracle import model as omodel
+from oracle import ops as oops
 from oracle.bf16 import bf16_bits_to_f32
 
 from _util import assert_close_rel, bits_of, f32_of, pkg
@@ -82,9 +83,10 @@ def check_greedy(records, what):
     return ties
 
 
-def test_tiny_model_teacher_forced(dev):
+@pytest.mark.parametrize("fused", [True, False])
+def test_tiny_model_teacher_forced(dev, fused):
     m = _m()
-    model = m.DecodeModel(tiny_cfg(), dev, seed=3, max_len=64, num_splits=2)
+    model = m.DecodeModel(tiny_cfg(), dev, seed=3, max_len=64, num_splits=2, fused=fused)
     oracle = oracle_from(model, num_splits=2)
     rng = np.random.default_rng(0)
     seq = rng.integers(0, model.cfg.vocab, 40)
@@ -111,12 +113,13 @@ def test_graph_replay_matches_eager(dev):
     assert np.all(eager[:7] == prompt.numpy())
 
 
-def test_full_size_layer_at_4096(dev):
+@pytest.mark.parametrize("fused", [True, False])
+def test_full_size_layer_at_4096(dev, fused):
     import torch
     m = _m()
     cfg = m.DecoderConfig(n_layers=1, vocab=512)
     L = 4096
-    model = m.DecodeModel(cfg, dev, seed=7, max_len=L + 128, num_splits=16)
+    model = m.DecodeModel(cfg, dev, seed=7, max_len=L + 128, num_splits=16, fused=fused)
     oracle = oracle_from(model, num_splits=16)
     rng = np.random.default_rng(7)
     pos = L - 1
@@ -136,17 +139,38 @@ def test_full_size_layer_at_4096(dev):
     st.positions.fill_(pos)
     st.seq_lens.fill_(pos + 1)
     st.slot_mapping.fill_(int(table[pos // cfg.block_size]) * cfg.block_size + pos % cfg.block_size)
-    h = torch.randn((1, cfg.hidden)).to(torch.bfloat16)
-    x = (3 * torch.randn((1, cfg.hidden))).to(torch.bfloat16)
-    model.h.copy_(h.to(dev))
+    x = (3 * torch.randn((1, cfg.hidden))).to(torch.bfloat16)  # layer 0 input: the embedding
     model.x.copy_(x.to(dev))
     model.layer_run(0)
+    # the next consumer (here the head) adds and normalises (down, residual)
+    y_dev, r_dev = pkg("native.torch_ops").add_rmsnorm(model.d, model.res_b, model.final_norm,
+                                                       cfg.eps)
     torch.cuda.synchronize()
     oracle.k[0] = kb.float().numpy()
     oracle.v[0] = vb.float().numpy()
-    y, res = oracle.layer(0, h.float().numpy()[0], x.float().numpy()[0], pos)
-    assert_close_rel(f32_of(model.x).reshape(-1), res, rtol=2e-2, atol_frac=2e-2, what="residual")
-    assert_close_rel(f32_of(model.h).reshape(-1), y, rtol=5e-2, atol_frac=5e-2, what="layer out")
+    xf = x.float().numpy()[0]
+    h0, _ = oops.add_rmsnorm(xf, None, f32_of(model.layers[0].input_norm), cfg.eps)
+    y, res = oracle.layer(0, h0, xf, pos)
+    assert_close_rel(f32_of(r_dev).reshape(-1), res, rtol=2e-2, atol_frac=2e-2, what="residual")
+    assert_close_rel(f32_of(y_dev).reshape(-1), y, rtol=5e-2, atol_frac=5e-2, what="layer out")
+
+
+@pytest.mark.parametrize("num_splits", [2, 3])
+def test_fused_and_unfused_steps_agree(dev, num_splits):
+    """The fused kernel sequence and the one-op-per-launch sequence give the
+    same greedy tokens and logits within bf16 noise."""
+    m = _m()
+    prompt_np = np.random.default_rng(4).integers(0, 1000, 9)
+    import torch
+    prompt = torch.tensor(prompt_np)
+    runs = []
+    for fused in (True, False):
+        model = m.DecodeModel(tiny_cfg(), dev, seed=6, max_len=64, num_splits=num_splits,
+                              fused=fused)
+        toks = model.generate(prompt, 25).cpu().numpy()
+        runs.append((toks, f32_of(model.logits).reshape(-1)))
+    np.testing.assert_array_equal(runs[0][0], runs[1][0])
+    assert_close_rel(runs[0][1], runs[1][1], rtol=2e-2, atol_frac=2e-2, what="final logits")
 
 
 def test_4b_model_greedy_tokens(dev):
