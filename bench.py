@@ -131,6 +131,49 @@ def attention_roofline(dev, reps: int, splits_list=(4, 8, 16, 32, 64)):
                                    "over a graph of 12 calls on rotating KV sets (302 MB)"}
 
 
+COPY_BYTES = 64 << 20
+
+
+def counter_workload(dev):
+    """Eager launches for a hardware-counter run (rocprofv3 --pmc): a plain
+    device copy of COPY_BYTES (the calibration kernel: it reads and writes
+    exactly COPY_BYTES), then the 9728x2560 GEMV over 24 rotating weight
+    sets, then split-KV decode + merge at context 6144 over 12 KV sets."""
+    import torch
+    from spark_vllm_ascend_amd.integration.weights import synthetic_q4_0
+    from spark_vllm_ascend_amd.native import torch_ops as ops
+    src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    ws = [synthetic_q4_0(GEMV_N, GEMV_K, 500 + i, dev) for i in range(24)]
+    x = torch.randn(GEMV_K, device=dev).to(torch.bfloat16)
+    y = torch.empty((1, GEMV_N), dtype=torch.bfloat16, device=dev)
+    for _ in range(2):
+        for w in ws:
+            ops.q4_0_gemv(x, w, GEMV_N, GEMV_K, out=y)
+    torch.cuda.synchronize()
+    del ws
+    n_q, n_kv, hd, bs = 32, 8, 128, 128
+    nblk = ATTN_CTX // bs
+    caches = [(torch.randn((nblk, bs, n_kv, hd), device=dev).to(torch.bfloat16),
+               torch.randn((nblk, bs, n_kv, hd), device=dev).to(torch.bfloat16))
+              for _ in range(12)]
+    table = torch.randperm(nblk, generator=torch.Generator().manual_seed(3)).to(torch.int32)
+    table = table.view(1, -1).to(dev)
+    q = torch.randn((1, n_q, hd), device=dev).to(torch.bfloat16)
+    seq_lens = torch.tensor([ATTN_CTX], dtype=torch.int32, device=dev)
+    S = 32
+    po = torch.empty((1, S, n_q, hd), dtype=torch.float32, device=dev)
+    pl = torch.empty((1, S, n_q), dtype=torch.float32, device=dev)
+    for kc, vc in caches:
+        ops.splitkv_decode_merged(q, kc, vc, table, seq_lens, S, hd ** -0.5, po, pl)
+    torch.cuda.synchronize()
+    return {"copy_bytes": COPY_BYTES, "gemv_bytes": GEMV_BYTES, "gemv_launches": 48,
+            "attn_launches": 12, "attn_splits": S}
+
+
 def build_model(dev, max_len: int, num_splits: int | None, seed: int = 0):
     from spark_vllm_ascend_amd.integration.model import DecodeModel, DecoderConfig
     return DecodeModel(DecoderConfig(), dev, seed=seed, max_len=max_len, num_splits=num_splits)
@@ -217,7 +260,8 @@ def main() -> int:
     ap.add_argument("--runs", type=int, default=3)
     ap.add_argument("--prompt-len", type=int, default=2048)
     ap.add_argument("--num-splits", type=int, default=0, help="0 = backend default")
-    ap.add_argument("--phase", choices=["all", "roofline", "decode"], default="all")
+    ap.add_argument("--phase", choices=["all", "roofline", "decode", "counters"], default="all",
+                    help="counters: eager launches for a rocprofv3 --pmc run, no timing")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     args = ap.parse_args()
@@ -232,6 +276,10 @@ def main() -> int:
     __graft_entry__.load_package()
     dev = torch.device("cuda:0")
     result = {}
+
+    if args.phase == "counters":
+        print(json.dumps(counter_workload(dev)))
+        return 0
 
     if args.phase in ("all", "roofline"):
         log("GEMV roofline (9728x2560, 24 rotating weight sets)")

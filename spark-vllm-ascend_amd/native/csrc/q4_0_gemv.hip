@@ -144,43 +144,51 @@ __global__ __launch_bounds__(512) void q4_0_gemv_kernel(GemvArgs a) {
   float* part = reinterpret_cast<float*>(lds + ks * (NPMAX * 8 * 36));
 
   // 1. This wave's activation chunks (16 bytes each, one per lane per group).
+  //    Every load of the kernel is issued unconditionally from a clamped,
+  //    always-valid address and masked afterwards: a load under a divergent
+  //    branch would make the compiler wait for all outstanding loads (the
+  //    weights included) before the first use of the activations.
   u32x4 xv[NPMAX], rv[NPMAX], gv[NPMAX];
+  bool xok[NPMAX];
   const u32x4* xg = reinterpret_cast<const u32x4*>(a.x);
+  const u32x4* rgp = reinterpret_cast<const u32x4*>(PRO && a.residual ? a.residual : a.x);
 #pragma unroll
   for (int t = 0; t < NPMAX; ++t) {
     const int c = (wave + ks * t) * 64 + lane;
-    const bool ok = c < nchunks;
-    xv[t] = ok ? xg[c] : u32x4{0u, 0u, 0u, 0u};
+    xok[t] = c < nchunks;
+    const int cc = min(c, nchunks - 1);
+    xv[t] = xg[cc];
     if constexpr (PRO) {
-      rv[t] = ok && a.residual ? reinterpret_cast<const u32x4*>(a.residual)[c]
-                               : u32x4{0u, 0u, 0u, 0u};
-      gv[t] = ok ? reinterpret_cast<const u32x4*>(a.gamma)[c] : u32x4{0u, 0u, 0u, 0u};
+      rv[t] = rgp[cc];
+      gv[t] = reinterpret_cast<const u32x4*>(a.gamma)[cc];
     }
   }
 
-  // 2. Every weight load of this wave.
+  // 2. Every weight load of this wave (rows past n_out and pairs past the
+  //    row end read the last valid row / pair; their results are dropped).
   constexpr int OUT_PER_GROUP = SWIGLU ? 4 : 8;
   int64_t wrow[RG];
-  bool row_ok[RG];
 #pragma unroll
   for (int g = 0; g < RG; ++g) {
     const int o = (blockIdx.x * RG + g) * OUT_PER_GROUP + (SWIGLU ? (rsub & 3) : rsub);
-    row_ok[g] = o < n_out;
-    wrow[g] = SWIGLU ? (o + ((rsub >> 2) ? a.up_offset_rows : 0)) : o;
+    const int oc = min(o, n_out - 1);
+    wrow[g] = SWIGLU ? (oc + ((rsub >> 2) ? a.up_offset_rows : 0)) : oc;
   }
   Pair wp[RG][NPMAX];
 #pragma unroll
   for (int g = 0; g < RG; ++g) {
 #pragma unroll
     for (int t = 0; t < NPMAX; ++t) {
-      const int j = (wave + ks * t) * 8 + col;
-      if (row_ok[g] && j < npairs) {
-        wp[g][t] = load_pair(a.w + wrow[g] * row_bytes + 36 * j);
-      } else {
-        wp[g][t].a = u32x4{0u, 0u, 0u, 0u};
-        wp[g][t].b = u32x4{0u, 0u, 0u, 0u};
-        wp[g][t].c = 0u;
-      }
+      const int j = min((wave + ks * t) * 8 + col, npairs - 1);
+      wp[g][t] = load_pair(a.w + wrow[g] * row_bytes + 36 * j);
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < NPMAX; ++t) {
+    if (!xok[t]) xv[t] = u32x4{0u, 0u, 0u, 0u};
+    if constexpr (PRO) {
+      if (!xok[t] || !a.residual) rv[t] = u32x4{0u, 0u, 0u, 0u};
+      if (!xok[t]) gv[t] = u32x4{0u, 0u, 0u, 0u};
     }
   }
 
