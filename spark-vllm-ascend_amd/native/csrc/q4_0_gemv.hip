@@ -400,32 +400,42 @@ struct GemvShape {
   int rg, ks, np;
 };
 
-static GemvShape pick_shape(int n_out, int out_per_group, int ngroups) {
+static GemvShape pick_shape(int n_out, int out_per_group, int ngroups, bool norm_swiglu) {
   GemvShape sh;
   const int wgs1 = (n_out + out_per_group - 1) / out_per_group;
   sh.rg = wgs1 >= 8192 ? 2 : 1;
+  // The norm prologue costs per workgroup (its activation loads and the
+  // cross-wave reduction): with the SwiGLU epilogue, 16 rows per workgroup
+  // and one pair group per wave measured fastest (9.5 vs 11.0 us at 9728x2560).
+  if (norm_swiglu && ngroups <= 8) sh.rg = 2;
   const int wgs = (wgs1 + sh.rg - 1) / sh.rg;
   // smallest np (<= 5 when possible) that still leaves >= 4 waves per SIMD
   int np = 1;
-  while (np < ngroups && np < 5 && (long)wgs * ((ngroups + np - 1) / np) > 8192) ++np;
+  while (!(norm_swiglu && ngroups <= 8) && np < ngroups && np < 5 &&
+         (long)wgs * ((ngroups + np - 1) / np) > 8192)
+    ++np;
   while ((ngroups + np - 1) / np > 8) ++np;
   sh.np = np;
   sh.ks = (ngroups + np - 1) / np;
   const char* e = getenv("SMX_GEMV_SHAPE");  // "rg,ks" override for tuning sweeps
   if (e) {
     int a = 0, b = 0;
-    if (sscanf(e, "%d,%d", &a, &b) == 2 && (a == 1 || a == 2) && b >= 1 && b <= 8) {
+    if (sscanf(e, "%d,%d", &a, &b) == 2 && (a == 1 || a == 2 || a == 4) && b >= 1 && b <= 8) {
       sh.rg = a;
       sh.ks = b < ngroups ? b : ngroups;
       sh.np = (ngroups + sh.ks - 1) / sh.ks;
     }
   }
+  if (sh.rg == 4 && sh.np > 2) sh.rg = 2;  // 4 row groups only with 1-2 pair groups (VGPRs)
   return sh;
 }
 
 template <int NPMAX, bool PRO, int EPI>
 static hipError_t dispatch_rg(hipStream_t s, const GemvArgs& a, const GemvShape& sh) {
-  if (sh.rg == 2) return launch_fast<NPMAX, 2, PRO, EPI>(s, a, sh.ks);
+  if constexpr (NPMAX <= 2) {
+    if (sh.rg == 4) return launch_fast<NPMAX, 4, PRO, EPI>(s, a, sh.ks);
+  }
+  if (sh.rg >= 2) return launch_fast<NPMAX, 2, PRO, EPI>(s, a, sh.ks);
   return launch_fast<NPMAX, 1, PRO, EPI>(s, a, sh.ks);
 }
 
@@ -446,10 +456,10 @@ static hipError_t dispatch_np(hipStream_t s, const GemvArgs& a, const GemvShape&
 
 // Whether the streaming kernel takes this call (else the generic kernel).
 static bool fast_path(int64_t k, const void* x, const void* w, GemvShape* sh, int64_t n_out,
-                      int out_per_group) {
+                      int out_per_group, bool norm_swiglu = false) {
   if (k % 64 != 0 || (uintptr_t)w % 4 != 0 || (uintptr_t)x % 16 != 0) return false;
   const int ngroups = (int)((k / 64 + 7) / 8);
-  *sh = pick_shape((int)n_out, out_per_group, ngroups);
+  *sh = pick_shape((int)n_out, out_per_group, ngroups, norm_swiglu);
   return sh->np <= 8;
 }
 
@@ -464,7 +474,8 @@ static hipError_t gemv_dispatch(hipStream_t s, GemvArgs a, int64_t k, int epi, b
   const int64_t nblocks = k / 32;
   a.npairs = (int)(nblocks / 2);
   GemvShape sh{1, 1, 1};
-  if (!fast_path(k, a.x, a.w, &sh, a.n_out, epi == EPI_SWIGLU ? 4 : 8)) {
+  if (!fast_path(k, a.x, a.w, &sh, a.n_out, epi == EPI_SWIGLU ? 4 : 8,
+                 pro && epi == EPI_SWIGLU)) {
     if (pro || epi == EPI_ARGMAX) return hipErrorInvalidValue;  // callers check first
     if (epi == EPI_SWIGLU)
       hipLaunchKernelGGL(q4_0_gemv_generic_kernel<true>, dim3((unsigned)a.n_out), dim3(64), 0, s,

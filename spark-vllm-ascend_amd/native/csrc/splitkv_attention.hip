@@ -87,14 +87,15 @@ struct SplitKVArgs {
 };
 
 // RMSNorm (gamma) + neox RoPE of one 128-wide head held by a wave as
-// (a, b) = dims (lane, lane + 64); returns the rotated pair as bf16 bits.
-__device__ __forceinline__ void norm_rope_head(float a, float b, const uint16_t* gamma, float c,
-                                               float sn, float eps, int lane, uint16_t* u_out,
+// (a, b) = dims (lane, lane + 64) with gamma (ga, gb) at the same dims;
+// returns the rotated pair as bf16 bits.
+__device__ __forceinline__ void norm_rope_head(float a, float b, float ga, float gb, float c,
+                                               float sn, float eps, uint16_t* u_out,
                                                uint16_t* v_out) {
   const float ss = wave_sum(a * a + b * b);
   const float inv = 1.0f / sqrtf(ss / (float)HD + eps);
-  const float an = round_bf16(a * inv * bf16_bits_to_f32(gamma[lane]));
-  const float bn = round_bf16(b * inv * bf16_bits_to_f32(gamma[lane + 64]));
+  const float an = round_bf16(a * inv * ga);
+  const float bn = round_bf16(b * inv * gb);
   *u_out = f32_to_bf16(an * c - bn * sn);
   *v_out = f32_to_bf16(bn * c + an * sn);
 }
@@ -131,53 +132,12 @@ __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(SplitKVArgs 
   const int bt0 = bt[w0 < cap ? (w0 >> bs_log2) : 0];
   const int bt1 = bt[w0 + 32 < cap ? ((w0 + 32) >> bs_log2) : 0];
   const int L = min(A.seq_lens[seq], cap);
-  // The new token (FUSEQ): its K/V are produced here by the workgroup whose
-  // split holds its position.
-  __shared__ __attribute__((aligned(16))) uint32_t kv_new[2][HD / 2];
   int64_t pos = 0;
-  bool owner = false;
-  if constexpr (FUSEQ) {
-    pos = A.positions[seq];
-    owner = pos >= s0 && pos < s0 + tps && pos < L;
-    const int nh = n_q + 2 * n_kv;
-    const uint16_t* row = A.q + (int64_t)seq * nh * HD;
-    const int64_t pc = pos < 0 ? 0 : (pos >= A.max_position ? A.max_position - 1 : pos);
-    const float c = bf16_bits_to_f32(A.cos_sin[pc * HD + lane]);
-    const float sn = bf16_bits_to_f32(A.cos_sin[pc * HD + 64 + lane]);
-    uint16_t* qh = reinterpret_cast<uint16_t*>(q_lds);
-    for (int h = wave; h < G; h += WAVES) {
-      const uint16_t* src = row + (kvh * G + h) * HD;
-      norm_rope_head(bf16_bits_to_f32(src[lane]), bf16_bits_to_f32(src[lane + 64]), A.q_gamma,
-                     c, sn, A.eps, lane, &qh[h * HD + lane], &qh[h * HD + 64 + lane]);
-    }
-    if (owner && wave == (G % WAVES)) {
-      const uint16_t* ksrc = row + (n_q + kvh) * HD;
-      const uint16_t* vsrc = row + (n_q + n_kv + kvh) * HD;
-      uint16_t* kn = reinterpret_cast<uint16_t*>(kv_new[0]);
-      uint16_t* vn = reinterpret_cast<uint16_t*>(kv_new[1]);
-      norm_rope_head(bf16_bits_to_f32(ksrc[lane]), bf16_bits_to_f32(ksrc[lane + 64]), A.k_gamma,
-                     c, sn, A.eps, lane, &kn[lane], &kn[lane + 64]);
-      vn[lane] = vsrc[lane];
-      vn[lane + 64] = vsrc[lane + 64];
-      const int64_t slot = A.slot_mapping[seq];
-      if (slot >= 0 && slot < ((int64_t)num_blocks << bs_log2)) {
-        uint16_t* kd = A.kc_w + (slot * n_kv + kvh) * HD;
-        uint16_t* vd = A.vc_w + (slot * n_kv + kvh) * HD;
-        kd[lane] = kn[lane];
-        kd[lane + 64] = kn[lane + 64];
-        vd[lane] = vsrc[lane];
-        vd[lane + 64] = vsrc[lane + 64];
-      }
-    }
-  } else {
-    if (tid < G * HD / 8)
-      reinterpret_cast<u32x4*>(q_lds)[tid] =
-          reinterpret_cast<const u32x4*>(A.q + ((int64_t)seq * n_q + kvh * G) * HD)[tid];
-  }
+  if constexpr (FUSEQ) pos = A.positions[seq];
   const int s1 = min(L, s0 + tps);
   float* po = part_o + (((int64_t)seq * num_splits + split) * n_q + kvh * G) * HD;
   float* pl = part_lse + ((int64_t)seq * num_splits + split) * n_q + kvh * G;
-  if (s0 >= s1) {
+  if (s0 >= s1) {  // empty split (uniform over the workgroup)
     for (int i = tid; i < G * HD; i += NT) po[i] = 0.f;
     if (tid < G) pl[tid] = -INFINITY;
     return;
@@ -192,6 +152,116 @@ __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(SplitKVArgs 
   const int hsel = lane & 3;                 // softmax: the head this lane keeps
   const int vt = lane >> 4, dv = lane & 15;  // PV: token slot, 8-dim slice
 
+  // A block-table entry outside [0, num_blocks) is never dereferenced: the
+  // page is replaced by page 0 and the partial is poisoned with NaN below.
+  // A wave without tokens still issues its first block's loads (from valid
+  // pages, results unused): loads under a branch would make the compiler
+  // wait for every outstanding load before the q prologue.
+  const bool has_work = w0 < w1;
+  bool bad_page = false;
+  auto half_base = [&](int t, int pg) -> int64_t {  // first token of a 32-token half
+    if ((unsigned)pg >= (unsigned)num_blocks) {
+      bad_page = bad_page || has_work;
+      pg = 0;
+    }
+    return (int64_t)pg * page_stride + (int64_t)(t & (bs - 1)) * tok_stride + kvh * HD;
+  };
+  // Every K and V load of one 64-token block; tokens past the chunk end are
+  // loaded from the block's first token (always valid) instead of branching,
+  // and their scores are masked to -inf.
+  u32x4 kr[8][2], vr[8][2];
+  auto load_block = [&](int t0) {
+    const int64_t b0 = half_base(t0, t0 == w0 ? bt0 : bt[t0 >> bs_log2]);
+    const int64_t b1 = t0 + 32 < w1
+                           ? half_base(t0 + 32, t0 == w0 ? bt1 : bt[(t0 + 32) >> bs_log2])
+                           : b0;
+    auto tok_off = [&](int t) -> int64_t {
+      const int te = t0 + t < w1 ? t : 0;
+      return (te < 32 ? b0 : b1) + (int64_t)(te & 31) * tok_stride;
+    };
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const uint16_t* p = kc + tok_off(8 * r + tok);
+      kr[r][0] = reinterpret_cast<const u32x4*>(p)[dq];
+      kr[r][1] = reinterpret_cast<const u32x4*>(p)[dq + 8];
+    }
+#pragma unroll
+    for (int jp = 0; jp < 8; ++jp)
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+        vr[jp][hf] = reinterpret_cast<const u32x4*>(vc + tok_off(8 * jp + vt + 4 * hf))[dv];
+  };
+  // The q prologue's inputs are loaded first and the first K/V block right
+  // after, so the prologue (and, fused, the q/k norm + RoPE + KV write) runs
+  // while the K/V block is in flight.
+  constexpr int HPW = (G + WAVES - 1) / WAVES;  // q heads per wave (FUSEQ)
+  __shared__ __attribute__((aligned(16))) uint32_t kv_new[2][HD / 2];
+  bool owner = false;
+  float qa[HPW], qb[HPW], qga = 0.f, qgb = 0.f, c = 0.f, sn = 0.f;
+  float ka = 0.f, kb = 0.f, kga = 0.f, kgb = 0.f;
+  uint16_t va = 0, vb = 0;
+  int64_t slot = -1;
+  const int nh = n_q + 2 * n_kv;
+  const uint16_t* row = A.q + (int64_t)seq * nh * HD;
+  u32x4 qv = u32x4{0u, 0u, 0u, 0u};
+  if constexpr (FUSEQ) {
+    owner = pos >= s0 && pos < s0 + tps && pos < L;
+    const int64_t pc = pos < 0 ? 0 : (pos >= A.max_position ? A.max_position - 1 : pos);
+#pragma unroll
+    for (int i = 0; i < HPW; ++i) {
+      const int h = min(wave + i * WAVES, G - 1);
+      qa[i] = bf16_bits_to_f32(row[(kvh * G + h) * HD + lane]);
+      qb[i] = bf16_bits_to_f32(row[(kvh * G + h) * HD + 64 + lane]);
+    }
+    qga = bf16_bits_to_f32(A.q_gamma[lane]);
+    qgb = bf16_bits_to_f32(A.q_gamma[lane + 64]);
+    c = bf16_bits_to_f32(A.cos_sin[pc * HD + lane]);
+    sn = bf16_bits_to_f32(A.cos_sin[pc * HD + 64 + lane]);
+    {  // the new token's k/v inputs (used by the owner's wave G % WAVES only)
+      ka = bf16_bits_to_f32(row[(n_q + kvh) * HD + lane]);
+      kb = bf16_bits_to_f32(row[(n_q + kvh) * HD + 64 + lane]);
+      kga = bf16_bits_to_f32(A.k_gamma[lane]);
+      kgb = bf16_bits_to_f32(A.k_gamma[lane + 64]);
+      va = row[(n_q + n_kv + kvh) * HD + lane];
+      vb = row[(n_q + n_kv + kvh) * HD + 64 + lane];
+      slot = A.slot_mapping[seq];
+    }
+  } else {
+    qv = reinterpret_cast<const u32x4*>(A.q + ((int64_t)seq * n_q + kvh * G) * HD)[lane];
+  }
+  load_block(w0);
+
+  if constexpr (FUSEQ) {
+    uint16_t* qh = reinterpret_cast<uint16_t*>(q_lds);
+#pragma unroll
+    for (int i = 0; i < HPW; ++i) {
+      const int h = wave + i * WAVES;
+      if (h < G)
+        norm_rope_head(qa[i], qb[i], qga, qgb, c, sn, A.eps, &qh[h * HD + lane],
+                       &qh[h * HD + 64 + lane]);
+    }
+    if (owner && wave == (G % WAVES)) {
+      uint16_t* kn = reinterpret_cast<uint16_t*>(kv_new[0]);
+      uint16_t* vn = reinterpret_cast<uint16_t*>(kv_new[1]);
+      uint16_t ku, kv2;
+      norm_rope_head(ka, kb, kga, kgb, c, sn, A.eps, &ku, &kv2);
+      kn[lane] = ku;
+      kn[lane + 64] = kv2;
+      vn[lane] = va;
+      vn[lane + 64] = vb;
+      if (slot >= 0 && slot < ((int64_t)num_blocks << bs_log2)) {
+        uint16_t* kd = A.kc_w + (slot * n_kv + kvh) * HD;
+        uint16_t* vd = A.vc_w + (slot * n_kv + kvh) * HD;
+        kd[lane] = ku;
+        kd[lane + 64] = kv2;
+        vd[lane] = va;
+        vd[lane + 64] = vb;
+      }
+    }
+  } else {
+    if (tid < G * HD / 8) reinterpret_cast<u32x4*>(q_lds)[tid] = qv;
+  }
+
   __syncthreads();
   u32x4 qr[G][2];
 #pragma unroll
@@ -199,17 +269,6 @@ __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(SplitKVArgs 
     qr[h][0] = reinterpret_cast<const u32x4*>(q_lds)[h * 16 + dq];
     qr[h][1] = reinterpret_cast<const u32x4*>(q_lds)[h * 16 + dq + 8];
   }
-
-  // A block-table entry outside [0, num_blocks) is never dereferenced: the
-  // page is replaced by page 0 and the partial is poisoned with NaN below.
-  bool bad_page = false;
-  auto half_base = [&](int t, int pg) -> int64_t {  // first token of a 32-token half
-    if ((unsigned)pg >= (unsigned)num_blocks) {
-      bad_page = true;
-      pg = 0;
-    }
-    return (int64_t)pg * page_stride + (int64_t)(t & (bs - 1)) * tok_stride + kvh * HD;
-  };
 
   float m_mine = -INFINITY;  // running max (log2 domain) of head hsel
   float l_lane = 0.f;        // running sum of head hsel over this lane's tokens
@@ -220,29 +279,7 @@ __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(SplitKVArgs 
     for (int i = 0; i < 8; ++i) o[h][i] = 0.f;
 
   for (int t0 = w0; t0 < w1; t0 += BLK) {
-    const int64_t b0 = half_base(t0, t0 == w0 ? bt0 : bt[t0 >> bs_log2]);
-    const int64_t b1 = t0 + 32 < w1
-                           ? half_base(t0 + 32, t0 == w0 ? bt1 : bt[(t0 + 32) >> bs_log2])
-                           : b0;
-    // Tokens past the chunk end are loaded from the block's first token
-    // (always valid) instead of branching; their scores are masked to -inf.
-    auto tok_off = [&](int t) -> int64_t {
-      const int te = t0 + t < w1 ? t : 0;
-      return (te < 32 ? b0 : b1) + (int64_t)(te & 31) * tok_stride;
-    };
-    u32x4 kr[8][2];
-#pragma unroll
-    for (int r = 0; r < 8; ++r) {
-      const uint16_t* p = kc + tok_off(8 * r + tok);
-      kr[r][0] = reinterpret_cast<const u32x4*>(p)[dq];
-      kr[r][1] = reinterpret_cast<const u32x4*>(p)[dq + 8];
-    }
-    u32x4 vr[8][2];
-#pragma unroll
-    for (int jp = 0; jp < 8; ++jp)
-#pragma unroll
-      for (int hf = 0; hf < 2; ++hf)
-        vr[jp][hf] = reinterpret_cast<const u32x4*>(vc + tok_off(8 * jp + vt + 4 * hf))[dv];
+    if (t0 != w0) load_block(t0);
 
     if constexpr (FUSEQ) {
       // The new token's K/V come from LDS (its cache slot is written by this
