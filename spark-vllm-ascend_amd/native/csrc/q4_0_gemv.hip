@@ -127,7 +127,7 @@ struct GemvArgs {
 //  EPI_ARGMAX: besides y, each workgroup writes the max (value, -index) key
 //       of its rows, for an on-device greedy argmax.
 template <int NPMAX, int RG, bool PRO, int EPI>
-__global__ __launch_bounds__(512) void q4_0_gemv_kernel(GemvArgs a) {
+__global__ __launch_bounds__(NPMAX <= 2 ? 1024 : 512) void q4_0_gemv_kernel(GemvArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
   constexpr bool SWIGLU = EPI == EPI_SWIGLU;
   const int ks = blockDim.x >> 6;
@@ -401,29 +401,32 @@ struct GemvShape {
 };
 
 static GemvShape pick_shape(int n_out, int out_per_group, int ngroups, bool norm_swiglu) {
+  // Measured on MI355X (graph-replayed launches over rotating weights):
+  //  * every pair group of a row gets its own wave (np = 1) up to 16 waves
+  //    per workgroup -- shorter per-wave work beats fewer, longer waves;
+  //  * 16 rows per workgroup (rg = 2) for long rows (K >= 4096), for very
+  //    tall matrices (the 151936-row head) and for the norm + SwiGLU
+  //    variant; 8 rows otherwise (6144/9728 x 2560).
   GemvShape sh;
   const int wgs1 = (n_out + out_per_group - 1) / out_per_group;
-  sh.rg = wgs1 >= 8192 ? 2 : 1;
-  // The norm prologue costs per workgroup (its activation loads and the
-  // cross-wave reduction): with the SwiGLU epilogue, 16 rows per workgroup
-  // and one pair group per wave measured fastest (9.5 vs 11.0 us at 9728x2560).
-  if (norm_swiglu && ngroups <= 8) sh.rg = 2;
-  const int wgs = (wgs1 + sh.rg - 1) / sh.rg;
-  // smallest np (<= 5 when possible) that still leaves >= 4 waves per SIMD
-  int np = 1;
-  while (!(norm_swiglu && ngroups <= 8) && np < ngroups && np < 5 &&
-         (long)wgs * ((ngroups + np - 1) / np) > 8192)
-    ++np;
-  while ((ngroups + np - 1) / np > 8) ++np;
-  sh.np = np;
-  sh.ks = (ngroups + np - 1) / np;
+  sh.rg = (ngroups >= 8 || wgs1 >= 8192 || norm_swiglu) ? 2 : 1;
+  sh.np = (ngroups + 15) / 16;
+  sh.ks = (ngroups + sh.np - 1) / sh.np;
+  if (sh.np > 2) {  // above 2 pair groups per lane, at most 8 waves per workgroup
+    sh.np = (ngroups + 7) / 8;
+    sh.ks = (ngroups + sh.np - 1) / sh.np;
+  }
   const char* e = getenv("SMX_GEMV_SHAPE");  // "rg,ks" override for tuning sweeps
   if (e) {
     int a = 0, b = 0;
-    if (sscanf(e, "%d,%d", &a, &b) == 2 && (a == 1 || a == 2 || a == 4) && b >= 1 && b <= 8) {
+    if (sscanf(e, "%d,%d", &a, &b) == 2 && (a == 1 || a == 2 || a == 4) && b >= 1 && b <= 16) {
       sh.rg = a;
       sh.ks = b < ngroups ? b : ngroups;
       sh.np = (ngroups + sh.ks - 1) / sh.ks;
+      if (sh.np > 2 && sh.ks > 8) {  // workgroups above 8 waves only with 1-2 pair groups
+        sh.ks = 8;
+        sh.np = (ngroups + 7) / 8;
+      }
     }
   }
   if (sh.rg == 4 && sh.np > 2) sh.rg = 2;  // 4 row groups only with 1-2 pair groups (VGPRs)
