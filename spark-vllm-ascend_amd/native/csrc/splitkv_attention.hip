@@ -49,7 +49,6 @@ __device__ __forceinline__ float max_stride4(float v) {
   return v;
 }
 
-constexpr int BLK = 64;  // tokens per wave block: all K and V loads of a block are issued at once
 
 // One workgroup of WAVES waves per (split, kv head, sequence).  Split s
 // covers [s*T, s*T + T) of the block table's capacity C (T = 32-aligned
@@ -100,8 +99,10 @@ __device__ __forceinline__ void norm_rope_head(float a, float b, float ga, float
   *v_out = f32_to_bf16(bn * c + an * sn);
 }
 
-template <int WAVES, bool FUSEQ>
+template <int WAVES, int BLK, bool FUSEQ>
 __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(SplitKVArgs A) {
+  static_assert(BLK == 32 || BLK == 64, "blocks of 32 or 64 tokens");
+  constexpr int RB = BLK / 8;  // 8-token steps per block
   const uint16_t* __restrict__ kc = A.kc;
   const uint16_t* __restrict__ vc = A.vc;
   const int32_t* __restrict__ block_table = A.block_table;
@@ -112,7 +113,7 @@ __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(SplitKVArgs 
   const float scale_log2 = A.scale_log2;
   constexpr int NT = 64 * WAVES;
   __shared__ __attribute__((aligned(16))) uint32_t q_lds[G * HD / 2];  // 4 heads, bf16 pairs
-  __shared__ __attribute__((aligned(16))) uint32_t p2[WAVES][128];     // [jp 8][vt 4][h 4]
+  __shared__ __attribute__((aligned(16))) uint32_t p2[WAVES][2 * BLK];  // [jp RB][vt 4][h 4]
   __shared__ float o_w[WAVES][G * HD];
   __shared__ float m_w[WAVES][G], l_w[WAVES][G];
   __shared__ int bad_w[WAVES];
@@ -169,10 +170,10 @@ __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(SplitKVArgs 
   // Every K and V load of one 64-token block; tokens past the chunk end are
   // loaded from the block's first token (always valid) instead of branching,
   // and their scores are masked to -inf.
-  u32x4 kr[8][2], vr[8][2];
+  u32x4 kr[RB][2], vr[RB][2];
   auto load_block = [&](int t0) {
     const int64_t b0 = half_base(t0, t0 == w0 ? bt0 : bt[t0 >> bs_log2]);
-    const int64_t b1 = t0 + 32 < w1
+    const int64_t b1 = BLK == 64 && t0 + 32 < w1
                            ? half_base(t0 + 32, t0 == w0 ? bt1 : bt[(t0 + 32) >> bs_log2])
                            : b0;
     auto tok_off = [&](int t) -> int64_t {
@@ -180,13 +181,13 @@ __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(SplitKVArgs 
       return (te < 32 ? b0 : b1) + (int64_t)(te & 31) * tok_stride;
     };
 #pragma unroll
-    for (int r = 0; r < 8; ++r) {
+    for (int r = 0; r < RB; ++r) {
       const uint16_t* p = kc + tok_off(8 * r + tok);
       kr[r][0] = reinterpret_cast<const u32x4*>(p)[dq];
       kr[r][1] = reinterpret_cast<const u32x4*>(p)[dq + 8];
     }
 #pragma unroll
-    for (int jp = 0; jp < 8; ++jp)
+    for (int jp = 0; jp < RB; ++jp)
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf)
         vr[jp][hf] = reinterpret_cast<const u32x4*>(vc + tok_off(8 * jp + vt + 4 * hf))[dv];
@@ -287,22 +288,22 @@ __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(SplitKVArgs 
       const int tp = (int)(pos - t0);
       if (owner && tp >= 0 && tp < BLK) {
 #pragma unroll
-        for (int r = 0; r < 8; ++r)
+        for (int r = 0; r < RB; ++r)
           if (8 * r + tok == tp) {
             kr[r][0] = reinterpret_cast<const u32x4*>(kv_new[0])[dq];
             kr[r][1] = reinterpret_cast<const u32x4*>(kv_new[0])[dq + 8];
           }
 #pragma unroll
-        for (int jp = 0; jp < 8; ++jp)
+        for (int jp = 0; jp < RB; ++jp)
 #pragma unroll
           for (int hf = 0; hf < 2; ++hf)
             if (8 * jp + vt + 4 * hf == tp) vr[jp][hf] = reinterpret_cast<const u32x4*>(kv_new[1])[dv];
       }
     }
     // ---- scores: token 8r + tok, head hsel
-    float sm[8];
+    float sm[RB];
 #pragma unroll
-    for (int r = 0; r < 8; ++r) {
+    for (int r = 0; r < RB; ++r) {
       float a[G];
 #pragma unroll
       for (int h = 0; h < G; ++h) {
@@ -322,7 +323,7 @@ __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(SplitKVArgs 
     // ---- online softmax (log2 domain) for head hsel
     float mx = sm[0];
 #pragma unroll
-    for (int r = 1; r < 8; ++r) mx = fmaxf(mx, sm[r]);
+    for (int r = 1; r < RB; ++r) mx = fmaxf(mx, sm[r]);
     mx = max_stride4(mx);
     const float mn = fmaxf(m_mine, mx);
     const float alpha = exp2f(m_mine - mn);
@@ -330,7 +331,7 @@ __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(SplitKVArgs 
     const bool writer = (lane & 4) == 0;  // lanes dq and dq + 4 hold the same head
     float psum = 0.f;
 #pragma unroll
-    for (int r = 0; r < 8; ++r) {
+    for (int r = 0; r < RB; ++r) {
       const float p = exp2f(sm[r] - mn);
       psum += p;
       if (writer) {
@@ -354,7 +355,7 @@ __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(SplitKVArgs 
 #pragma unroll
       for (int i = 0; i < 8; ++i) o[h][i] *= alpha_h[h];
 #pragma unroll
-    for (int jp = 0; jp < 8; ++jp) {
+    for (int jp = 0; jp < RB; ++jp) {
       const u32x4 pp = *reinterpret_cast<const u32x4*>(&p2[wave][(jp * 4 + vt) * 4]);
       const u32x4 va = vr[jp][0], vb2 = vr[jp][1];
       uint32_t vpair[8];  // (v[t1][d], v[t2][d]) for the 8 dims
@@ -501,20 +502,34 @@ int launch_splitkv(void* stream, smx::SplitKVArgs a, int32_t num_seqs, int32_t b
   while ((1 << bs_log2) < block_size) ++bs_log2;
   a.bs_log2 = bs_log2;
   a.scale_log2 = scale * 1.44269504088896340736f;
-  // One 64-token block per wave: the wave count follows the split size.
+  // Blocks of 32 tokens (shorter per-wave dependency chains) while a split
+  // fits 8 such waves, else 64-token blocks over 8 waves.
   const int64_t cap = (int64_t)a.max_blocks * block_size;
   const int64_t tps = ((cap + a.num_splits - 1) / a.num_splits + 31) / 32 * 32;
-  int waves = tps <= 64 ? 1 : tps <= 128 ? 2 : tps <= 256 ? 4 : 8;
-  const char* e = getenv("SMX_ATTN_WAVES");  // override for tuning sweeps
-  if (e && (atoi(e) == 1 || atoi(e) == 2 || atoi(e) == 4 || atoi(e) == 8)) waves = atoi(e);
+  int blk = tps <= 256 ? 32 : 64;
+  int waves = blk == 64 ? 8 : tps <= 32 ? 1 : tps <= 64 ? 2 : tps <= 128 ? 4 : 8;
+  const char* e = getenv("SMX_ATTN_WAVES");  // "waves[,blk]" override for tuning sweeps
+  if (e) {
+    int w = 0, b = 0;
+    const int n = sscanf(e, "%d,%d", &w, &b);
+    if (n >= 1 && (w == 1 || w == 2 || w == 4 || w == 8)) waves = w;
+    if (n == 2 && (b == 32 || b == 64)) blk = b;
+  }
   const dim3 grid(a.num_splits, a.n_kv, num_seqs);
-#define SMX_ATTN_LAUNCH(W)                                                                      \
-  hipLaunchKernelGGL((smx::splitkv_decode_kernel<W, FUSEQ>), grid, dim3(64 * W), 0,             \
+#define SMX_ATTN_LAUNCH(W, B)                                                                   \
+  hipLaunchKernelGGL((smx::splitkv_decode_kernel<W, B, FUSEQ>), grid, dim3(64 * W), 0,          \
                      (hipStream_t)stream, a)
-  if (waves == 8) SMX_ATTN_LAUNCH(8);
-  else if (waves == 4) SMX_ATTN_LAUNCH(4);
-  else if (waves == 2) SMX_ATTN_LAUNCH(2);
-  else SMX_ATTN_LAUNCH(1);
+  if (blk == 32) {
+    if (waves == 8) SMX_ATTN_LAUNCH(8, 32);
+    else if (waves == 4) SMX_ATTN_LAUNCH(4, 32);
+    else if (waves == 2) SMX_ATTN_LAUNCH(2, 32);
+    else SMX_ATTN_LAUNCH(1, 32);
+  } else {
+    if (waves == 8) SMX_ATTN_LAUNCH(8, 64);
+    else if (waves == 4) SMX_ATTN_LAUNCH(4, 64);
+    else if (waves == 2) SMX_ATTN_LAUNCH(2, 64);
+    else SMX_ATTN_LAUNCH(1, 64);
+  }
 #undef SMX_ATTN_LAUNCH
   return (int)hipGetLastError();
 }
