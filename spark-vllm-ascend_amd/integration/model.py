@@ -192,6 +192,21 @@ class DecodeModel:
                             else None)
         self.graph: torch.cuda.CUDAGraph | None = None
 
+    @classmethod
+    def from_gguf(cls, path, device, max_len: int = 8192, num_splits: int | None = None,
+                  block_size: int = 128, fused: bool = True) -> "DecodeModel":
+        """A model whose weights come from a local GGUF file (Q4_0 linears and
+        head, float norms rounded to bf16), shapes from its metadata."""
+        from .gguf_file import GGUFFile, decoder_config, decoder_weights
+        g = GGUFFile(path)
+        cfg = DecoderConfig(**decoder_config(g), block_size=block_size)
+        dev = torch.device(device)
+        w = {}
+        for k, v in decoder_weights(g, cfg.n_layers).items():
+            t = torch.from_numpy(v.copy())
+            w[k] = (t.to(torch.bfloat16) if t.dtype == torch.float32 else t).to(dev)
+        return cls(cfg, dev, max_len=max_len, num_splits=num_splits, weights=w, fused=fused)
+
     # ------------------------------------------------------------------ step
     def _layer_input(self, i: int):
         """(activation, residual) entering layer i: the embedding alone for
