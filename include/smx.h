@@ -264,6 +264,21 @@ int smx_argmax_bf16(void* stream, const void* logits, int64_t rows,
                     int64_t vocab, int64_t* out_ids);
 
 /*
+ * Slot mapping of a ragged batch (vLLM's compute_slot_mapping for one KV
+ * group): token t of request r (query_start_loc[r] <= t <
+ * query_start_loc[r + 1], int32 [num_reqs + 1]) at positions[t] gets
+ * block_table[r][p / block_size] * block_size + p % block_size; tokens past
+ * the table or at negative positions get -1, and the whole padded output
+ * [max_tokens] is written (entries num_tokens.. are -1).  Replaces
+ * _slot_one / slot4_kernel (src/spark_vllm_ascend/integration/
+ * slot_mapping.py:8-33), which covers one request per call.
+ */
+int smx_compute_slot_mapping(void* stream, const int32_t* query_start_loc, int32_t num_reqs,
+                             const int64_t* positions, const int32_t* block_table,
+                             int64_t* slot_mapping, int32_t num_tokens, int32_t max_tokens,
+                             int32_t max_blocks, int32_t block_size);
+
+/*
  * Paged KV write (vLLM reshape_and_cache): for each token t with
  * slot_mapping[t] in [0, num_blocks * block_size), copy key[t] and value[t]
  * ([n_kv, head_dim] bf16 each) into k_cache / v_cache at that slot;

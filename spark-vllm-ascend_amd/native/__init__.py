@@ -39,6 +39,7 @@ SIGNATURES = {
                                               _P, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32,
                                               _I32, _F32, _F32],
     "smx_lse_merge": [_P, _P, _P, _P, _I32, _I32, _I32, _I32],
+    "smx_compute_slot_mapping": [_P, _P, _I32, _P, _P, _P, _I32, _I32, _I32, _I32],
     "smx_add_rmsnorm": [_P, _P, _P, _P, _P, _P, _I64, _I64, _F32],
     "smx_qknorm_rope_kv_write": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32,
                                  _I32, _I32, _I32, _F32],

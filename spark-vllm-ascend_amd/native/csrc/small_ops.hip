@@ -264,6 +264,35 @@ __global__ __launch_bounds__(64) void reshape_and_cache_kernel(
   }
 }
 
+// Slot of every token of a (ragged) batch: token t of request r (the r with
+// query_start_loc[r] <= t < query_start_loc[r + 1]) at position p goes to
+// block_table[r][p / block_size] * block_size + p % block_size; tokens in no
+// request, past the block table or at a negative position get -1, and so do
+// the padding entries num_tokens <= t < max_tokens.
+__global__ __launch_bounds__(256) void slot_mapping_kernel(
+    const int32_t* __restrict__ query_start_loc, int num_reqs,
+    const int64_t* __restrict__ positions, const int32_t* __restrict__ block_table,
+    int64_t* __restrict__ out, int num_tokens, int max_tokens, int max_blocks, int block_size) {
+  const int t = blockIdx.x * 256 + threadIdx.x;
+  if (t >= max_tokens) return;
+  int64_t v = -1;
+  if (t < num_tokens) {
+    int lo = 0, hi = num_reqs;  // last r with query_start_loc[r] <= t
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (query_start_loc[mid] <= t) lo = mid;
+      else hi = mid;
+    }
+    if (query_start_loc[lo] <= t && t < query_start_loc[lo + 1]) {
+      const int64_t pos = positions[t];
+      const int64_t blk = pos / block_size;
+      if (pos >= 0 && blk < max_blocks)
+        v = (int64_t)block_table[(int64_t)lo * max_blocks + blk] * block_size + pos % block_size;
+    }
+  }
+  out[t] = v;
+}
+
 }  // namespace
 }  // namespace smx
 
@@ -382,5 +411,25 @@ extern "C" int smx_decode_advance(void* stream, int64_t* next_ids, const uint64_
                      (hipStream_t)stream, next_ids, argmax_keys, num_keys, forced_ids, forced_len,
                      ids, positions, seq_lens, slot_mapping, block_table, tokens_out, max_blocks,
                      block_size, max_len);
+  return (int)hipGetLastError();
+}
+
+extern "C" int smx_compute_slot_mapping(void* stream, const int32_t* query_start_loc,
+                                        int32_t num_reqs, const int64_t* positions,
+                                        const int32_t* block_table, int64_t* slot_mapping,
+                                        int32_t num_tokens, int32_t max_tokens,
+                                        int32_t max_blocks, int32_t block_size) {
+  SMX_REQUIRE(query_start_loc && positions && block_table && slot_mapping,
+              "null pointer argument");
+  SMX_REQUIRE(num_reqs >= 1, "num_reqs must be >= 1");
+  SMX_REQUIRE(num_tokens >= 0 && max_tokens >= 1 && num_tokens <= max_tokens,
+              "need 0 <= num_tokens <= max_tokens, max_tokens >= 1");
+  SMX_REQUIRE(max_blocks >= 1 && block_size >= 1, "max_blocks and block_size must be >= 1");
+  SMX_REQUIRE((uintptr_t)positions % 8 == 0 && (uintptr_t)slot_mapping % 8 == 0 &&
+                  (uintptr_t)query_start_loc % 4 == 0 && (uintptr_t)block_table % 4 == 0,
+              "misaligned pointer");
+  hipLaunchKernelGGL(smx::slot_mapping_kernel, dim3((max_tokens + 255) / 256), dim3(256), 0,
+                     (hipStream_t)stream, query_start_loc, num_reqs, positions, block_table,
+                     slot_mapping, num_tokens, max_tokens, max_blocks, block_size);
   return (int)hipGetLastError();
 }

@@ -396,3 +396,28 @@ def qknorm_rope_splitkv_decode_merged(qkv: torch.Tensor, q_gamma: torch.Tensor,
          block_table.shape[1], num_blocks, bs, n_q, n_kv, hd, cos_sin.shape[0], float(eps),
          float(scale))
     return out
+
+
+def compute_slot_mapping(query_start_loc: torch.Tensor, positions: torch.Tensor,
+                         block_table: torch.Tensor, block_size: int, max_tokens: int | None = None,
+                         out: torch.Tensor | None = None) -> torch.Tensor:
+    """int64 slots [max_tokens] of a ragged batch (-1 for padding and for
+    positions past the block table)."""
+    num_reqs = query_start_loc.numel() - 1
+    _need(num_reqs >= 1, "query_start_loc needs num_reqs + 1 entries")
+    _check(query_start_loc, "query_start_loc", torch.int32)
+    _need(positions.dtype == torch.int64 and positions.device == query_start_loc.device
+          and positions.is_contiguous(), "positions must be contiguous int64 on the same device")
+    _check(block_table, "block_table", torch.int32, device=query_start_loc.device)
+    _need(block_table.dim() == 2 and block_table.shape[0] >= num_reqs, "block_table must be [reqs, max_blocks]")
+    num_tokens = positions.numel()
+    max_tokens = num_tokens if max_tokens is None else max_tokens
+    if out is None:
+        out = torch.empty(max(max_tokens, 1), dtype=torch.int64, device=positions.device)
+    _check(out, "out", torch.int64, device=positions.device)
+    _need(out.numel() >= max_tokens, "out must hold max_tokens entries")
+    pos_ptr = positions.data_ptr() if num_tokens else out.data_ptr()  # never read when empty
+    call("smx_compute_slot_mapping", _stream(out), query_start_loc.data_ptr(), num_reqs,
+         pos_ptr, block_table.data_ptr(), out.data_ptr(), num_tokens,
+         max(max_tokens, 1), block_table.shape[1], block_size)
+    return out
