@@ -279,6 +279,25 @@ int smx_compute_slot_mapping(void* stream, const int32_t* query_start_loc, int32
                              int32_t max_blocks, int32_t block_size);
 
 /*
+ * Q4_0 GEMM for m <= 16 activation rows (batched decode): y[m, n] = x[m, k]
+ * W^T with W GGUF Q4_0 [n, k/32] blocks, fp32 accumulation, bf16 out;
+ * k % 64 == 0, x 8-byte aligned.  The reference computes the same product
+ * one token at a time (GemvStage, src/spark_vllm_ascend/kernels/
+ * linear.py:16-200); the batched form is its multi-sequence extension.
+ */
+int smx_q4_0_gemm(void* stream, const void* x, const void* w, void* y, int64_t m, int64_t n,
+                  int64_t k);
+
+/*
+ * smx_q4_0_gemm with the SwiGLU epilogue: w holds 2d rows (gate rows 0..d-1,
+ * up rows d..2d-1); out[m, j] = bf16(silu(bf16(g)) * bf16(u)).  Replaces
+ * NativeUp.execute + activate_native (src/spark_vllm_ascend/kernels/
+ * linear.py:540-611) for several rows, with SwiGLU in place of GELU.
+ */
+int smx_q4_0_gemm_swiglu(void* stream, const void* x, const void* w, void* out, int64_t m,
+                         int64_t d, int64_t k);
+
+/*
  * Paged KV write (vLLM reshape_and_cache): for each token t with
  * slot_mapping[t] in [0, num_blocks * block_size), copy key[t] and value[t]
  * ([n_kv, head_dim] bf16 each) into k_cache / v_cache at that slot;

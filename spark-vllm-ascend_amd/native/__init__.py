@@ -39,6 +39,8 @@ SIGNATURES = {
                                               _P, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32,
                                               _I32, _F32, _F32],
     "smx_lse_merge": [_P, _P, _P, _P, _I32, _I32, _I32, _I32],
+    "smx_q4_0_gemm": [_P, _P, _P, _P, _I64, _I64, _I64],
+    "smx_q4_0_gemm_swiglu": [_P, _P, _P, _P, _I64, _I64, _I64],
     "smx_compute_slot_mapping": [_P, _P, _I32, _P, _P, _P, _I32, _I32, _I32, _I32],
     "smx_add_rmsnorm": [_P, _P, _P, _P, _P, _P, _I64, _I64, _F32],
     "smx_qknorm_rope_kv_write": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32,

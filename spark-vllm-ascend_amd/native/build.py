@@ -28,7 +28,7 @@ COMMON = [
     "-Wno-unused-function",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
-SOURCES = ["q4_0_gemv.hip", "splitkv_attention.hip", "small_ops.hip", "abi.cpp"]
+SOURCES = ["q4_0_gemv.hip", "q4_0_gemm.hip", "splitkv_attention.hip", "small_ops.hip", "abi.cpp"]
 
 
 def _compile(src: str) -> Path:

@@ -421,3 +421,32 @@ def compute_slot_mapping(query_start_loc: torch.Tensor, positions: torch.Tensor,
          pos_ptr, block_table.data_ptr(), out.data_ptr(), num_tokens,
          max(max_tokens, 1), block_table.shape[1], block_size)
     return out
+
+
+def q4_0_gemm(x: torch.Tensor, w: torch.Tensor, n: int, k: int,
+              out: torch.Tensor | None = None) -> torch.Tensor:
+    """y [m, n] = x [m, k] . W^T for m <= 16 rows (MFMA kernel)."""
+    _need(x.dim() == 2 and x.shape[1] == k and 1 <= x.shape[0] <= 16, "x must be [m <= 16, k]")
+    _check(x, "x", BF16)
+    _need(x.data_ptr() % 8 == 0, "x must be 8-byte aligned")
+    _check(w, "w", torch.uint8, n * q4_0_row_bytes(k), x.device)
+    if out is None:
+        out = torch.empty((x.shape[0], n), dtype=BF16, device=x.device)
+    _check(out, "out", BF16, x.shape[0] * n, x.device)
+    call("smx_q4_0_gemm", _stream(x), x.data_ptr(), w.data_ptr(), out.data_ptr(), x.shape[0], n, k)
+    return out
+
+
+def q4_0_gemm_swiglu(x: torch.Tensor, w: torch.Tensor, d: int, k: int,
+                     out: torch.Tensor | None = None) -> torch.Tensor:
+    """out [m, d] = silu(x W_gate^T) * (x W_up^T), W = [gate; up] [2d, k]."""
+    _need(x.dim() == 2 and x.shape[1] == k and 1 <= x.shape[0] <= 16, "x must be [m <= 16, k]")
+    _check(x, "x", BF16)
+    _need(x.data_ptr() % 8 == 0, "x must be 8-byte aligned")
+    _check(w, "w", torch.uint8, 2 * d * q4_0_row_bytes(k), x.device)
+    if out is None:
+        out = torch.empty((x.shape[0], d), dtype=BF16, device=x.device)
+    _check(out, "out", BF16, x.shape[0] * d, x.device)
+    call("smx_q4_0_gemm_swiglu", _stream(x), x.data_ptr(), w.data_ptr(), out.data_ptr(),
+         x.shape[0], d, k)
+    return out

@@ -73,6 +73,9 @@ def test_bindings_cover_header():
     ("smx_q4_0_add_rmsnorm_gemv_argmax", (None, 16, 32, 16, 16, 16, 16, 3, 64, 256, 1e-6)),
     ("smx_reshape_and_cache", (None, 16, 16, 16, 16, 16, 0, 8, 128, 4, 128)),
     ("smx_compute_slot_mapping", (None, 16, 1, 16, 16, 16, 5, 4, 8, 128)),
+    ("smx_q4_0_gemm", (None, 16, 16, 16, 17, 64, 256)),
+    ("smx_q4_0_gemm", (None, 16, 16, 16, 4, 64, 96)),
+    ("smx_q4_0_gemm_swiglu", (None, 12, 16, 16, 4, 64, 256)),
     ("smx_compute_slot_mapping", (None, 16, 0, 16, 16, 16, 1, 4, 8, 128)),
     ("smx_qknorm_rope_splitkv_decode_merged",
      (None, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16, 1, 4, 8, 8, 128, 32, 8, 128, 0, 1e-6, 0.1)),

@@ -1,0 +1,95 @@
+"""GPU parity of the batched Q4_0 GEMM (MFMA) through the C ABI: each output
+row within 1e-2 relative of the float64 oracle GEMV of that activation row;
+one-hot activations select dequantised weights bit-exactly (this pins the
+MFMA operand and result layouts); SwiGLU epilogue; writes stay in bounds."""
+import numpy as np
+import pytest
+
+from oracle import q4_0 as oq
+from oracle.bf16 import bf16_bits_to_f32, f32_to_bf16_bits
+from oracle.ops import silu_mul as o_silu_mul
+
+from _util import assert_close_rel, bf16_dev, bits_of, f32_of, pkg, randn_bf16
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dev():
+    import torch
+    return torch.device("cuda:0")
+
+
+@pytest.fixture(scope="module")
+def ops():
+    return pkg("native.torch_ops")
+
+
+def _w(blocks, dev):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(blocks).reshape(-1)).to(dev)
+
+
+@pytest.mark.parametrize("m", [1, 2, 5, 8, 16])
+@pytest.mark.parametrize("n,k", [(64, 256), (1000, 2560), (2560, 9728), (9728, 2560), (2560, 4096)])
+def test_gemm_vs_oracle(ops, dev, m, n, k):
+    if m in (2, 5) and n * k > 3_000_000:
+        pytest.skip("covered by other row counts")
+    rng = np.random.default_rng(m * 100 + n + k)
+    blocks = oq.make_blocks(n, k, seed=n + k)
+    x = randn_bf16(rng, (m, k))
+    y = f32_of(ops.q4_0_gemm(bf16_dev(x, dev), _w(blocks, dev), n, k)).reshape(m, n)
+    for r in range(m):
+        assert_close_rel(y[r], oq.gemv_f64(x[r], blocks, n, k), rtol=1e-2, atol_frac=5e-3,
+                         what=f"row {r}")
+
+
+def test_gemm_one_hot_layout(ops, dev):
+    """Row m of x is one-hot at column c_m: y[m][n] = bf16(dequant(W)[n][c_m])
+    exactly, for 16 rows, 48 output rows and columns spread over both blocks
+    of a pair and all nibble positions."""
+    n, k, m = 48, 256, 16
+    blocks = oq.make_blocks(n, k, seed=11, scale=1.0)
+    cols = np.array([0, 1, 14, 15, 16, 17, 30, 31, 32, 33, 46, 47, 48, 63, 100, 255])
+    x = np.zeros((m, k), dtype=np.uint16)
+    x[np.arange(m), cols] = f32_to_bf16_bits(np.float32([1.0]))[0]
+    y = bits_of(ops.q4_0_gemm(bf16_dev(x, dev), _w(blocks, dev), n, k)).reshape(m, n)
+    wq = oq.dequant_f32(blocks, n, k)
+    exp = f32_to_bf16_bits(wq[:, cols].T.copy())
+    np.testing.assert_array_equal(y, exp)
+
+
+@pytest.mark.parametrize("m,d,k", [(8, 9728, 2560), (3, 100, 256), (16, 64, 512)])
+def test_gemm_swiglu(ops, dev, m, d, k):
+    rng = np.random.default_rng(d + m)
+    blocks = oq.make_blocks(2 * d, k, seed=d + 1)
+    x = randn_bf16(rng, (m, k))
+    out = f32_of(ops.q4_0_gemm_swiglu(bf16_dev(x, dev), _w(blocks, dev), d, k)).reshape(m, d)
+    for r in range(m):
+        gu = oq.gemv_f64(x[r], blocks, 2 * d, k).astype(np.float32)
+        g = bf16_bits_to_f32(f32_to_bf16_bits(gu[:d]))
+        u = bf16_bits_to_f32(f32_to_bf16_bits(gu[d:]))
+        assert_close_rel(out[r], o_silu_mul(g, u), rtol=2e-2, atol_frac=5e-3, what=f"row {r}")
+
+
+def test_gemm_output_sentinels(ops, dev):
+    import torch
+    m, n, k = 3, 1000, 256
+    rng = np.random.default_rng(4)
+    blocks = oq.make_blocks(n, k, seed=4)
+    x = bf16_dev(randn_bf16(rng, (m, k)), dev)
+    guard = torch.full((m * n + 64,), 17.0, dtype=torch.bfloat16, device=dev)
+    y = guard[32:32 + m * n]
+    ops.q4_0_gemm(x, _w(blocks, dev), n, k, out=y)
+    gv = guard.float().cpu().numpy()
+    assert np.all(gv[:32] == 17.0) and np.all(gv[32 + m * n:] == 17.0)
+    assert np.all(np.isfinite(gv[32:32 + m * n]))
+
+
+def test_gemm_rejects_bad_arguments(ops, dev):
+    import torch
+    w = torch.zeros(64 * 8 * 18, dtype=torch.uint8, device=dev)
+    with pytest.raises(ValueError):
+        ops.q4_0_gemm(torch.zeros((17, 256), dtype=torch.bfloat16, device=dev), w, 64, 256)
+    with pytest.raises(ValueError):
+        ops.q4_0_gemm(torch.zeros((2, 256), dtype=torch.float32, device=dev), w, 64, 256)
