@@ -106,20 +106,26 @@ class DecodeState:
 
 
 class DecodeModel:
-    """A batch-1 Q4_0 decoder with random-init weights of a given shape."""
+    """A Q4_0 decoder with random-init weights of a given shape, decoding
+    `batch` sequences per step (one token each).  batch == 1 runs the fused
+    GEMV path; batch > 1 runs the MFMA GEMM (m = batch rows) with separate
+    norm launches, over a block table with one row per sequence."""
 
     def __init__(self, cfg: DecoderConfig, device, seed: int = 0, max_len: int = 8192,
                  num_splits: int | None = None, weights: dict | None = None,
-                 fused: bool = True):
+                 fused: bool = True, batch: int = 1):
+        if not 1 <= batch <= 16:
+            raise ValueError("batch must be in [1, 16]")
         self.cfg = cfg
-        self.fused = fused
+        self.batch = B = batch
+        self.fused = fused and batch == 1
         self.device = torch.device(device)
         self.max_len = max_len
         c = cfg
         gen = torch.Generator(device=self.device)
         gen.manual_seed(seed)
         blocks_per_seq = -(-max_len // c.block_size)
-        self.num_blocks = blocks_per_seq + 1
+        self.num_blocks = B * blocks_per_seq + 1
         self.layers: list[DecoderLayer] = []
         for i in range(c.n_layers):
             s = seed * 1000 + i * 10
@@ -157,37 +163,37 @@ class DecodeModel:
 
         # pages are handed out in a seeded shuffled order, to exercise paging
         perm = torch.randperm(self.num_blocks, generator=torch.Generator().manual_seed(seed))
-        table = perm[:blocks_per_seq].to(torch.int32).view(1, -1)
+        table = perm[:B * blocks_per_seq].to(torch.int32).view(B, -1)
         dev = self.device
         self.state = DecodeState(
-            ids=torch.zeros(1, dtype=torch.int64, device=dev),
-            positions=torch.zeros(1, dtype=torch.int64, device=dev),
-            seq_lens=torch.ones(1, dtype=torch.int32, device=dev),
-            slot_mapping=torch.zeros(1, dtype=torch.int64, device=dev),
+            ids=torch.zeros(B, dtype=torch.int64, device=dev),
+            positions=torch.zeros(B, dtype=torch.int64, device=dev),
+            seq_lens=torch.ones(B, dtype=torch.int32, device=dev),
+            slot_mapping=torch.zeros(B, dtype=torch.int64, device=dev),
             block_table=table.to(dev),
-            next_ids=torch.zeros(1, dtype=torch.int64, device=dev),
-            forced=torch.zeros((1, max_len), dtype=torch.int64, device=dev),
-            forced_len=torch.zeros(1, dtype=torch.int32, device=dev),
-            tokens=torch.full((1, max_len), -1, dtype=torch.int64, device=dev),
+            next_ids=torch.zeros(B, dtype=torch.int64, device=dev),
+            forced=torch.zeros((B, max_len), dtype=torch.int64, device=dev),
+            forced_len=torch.zeros(B, dtype=torch.int32, device=dev),
+            tokens=torch.full((B, max_len), -1, dtype=torch.int64, device=dev),
         )
         # activations (fixed addresses for graph capture)
         bf = dict(dtype=torch.bfloat16, device=dev)
-        self.x = torch.empty((1, c.hidden), **bf)         # embedding of the input id
-        self.res_a = torch.empty((1, c.hidden), **bf)     # residual after the attention add
-        self.res_b = torch.empty((1, c.hidden), **bf)     # residual after the MLP add
-        self.d = torch.empty((1, c.hidden), **bf)         # down projection output
-        self.h = torch.empty((1, c.hidden), **bf)         # normalised input (fused=False)
-        self.qkv_out = torch.empty((1, c.qkv_rows), **bf)
-        self.q = torch.empty((1, c.n_q, c.head_dim), **bf)
-        self.attn = torch.empty((1, c.n_q, c.head_dim), **bf)
-        self.o = torch.empty((1, c.hidden), **bf)
-        self.h2 = torch.empty((1, c.hidden), **bf)
-        self.act = torch.empty((1, c.intermediate), **bf)
-        self.logits = torch.empty((1, c.vocab), **bf)
-        self.partial_o = torch.empty((1, self.num_splits, c.n_q, c.head_dim), dtype=torch.float32,
+        self.x = torch.empty((B, c.hidden), **bf)         # embedding of the input id
+        self.res_a = torch.empty((B, c.hidden), **bf)     # residual after the attention add
+        self.res_b = torch.empty((B, c.hidden), **bf)     # residual after the MLP add
+        self.d = torch.empty((B, c.hidden), **bf)         # down projection output
+        self.h = torch.empty((B, c.hidden), **bf)         # normalised input (unfused)
+        self.qkv_out = torch.empty((B, c.qkv_rows), **bf)
+        self.q = torch.empty((B, c.n_q, c.head_dim), **bf)
+        self.attn = torch.empty((B, c.n_q, c.head_dim), **bf)
+        self.o = torch.empty((B, c.hidden), **bf)
+        self.h2 = torch.empty((B, c.hidden), **bf)
+        self.act = torch.empty((B, c.intermediate), **bf)
+        self.logits = torch.empty((B, c.vocab), **bf)
+        self.partial_o = torch.empty((B, self.num_splits, c.n_q, c.head_dim), dtype=torch.float32,
                                      device=dev)
-        self.partial_lse = torch.empty((1, self.num_splits, c.n_q), dtype=torch.float32, device=dev)
-        nk = torch_ops.argmax_keys_size(c.vocab, c.hidden)
+        self.partial_lse = torch.empty((B, self.num_splits, c.n_q), dtype=torch.float32, device=dev)
+        nk = torch_ops.argmax_keys_size(c.vocab, c.hidden) if B == 1 else 0
         self.argmax_keys = (torch.empty((1, nk), dtype=torch.int64, device=dev) if nk > 0
                             else None)
         self.graph: torch.cuda.CUDAGraph | None = None
@@ -231,6 +237,24 @@ class DecodeModel:
             ops.add_rmsnorm_gemv_swiglu(self.o, self.res_a, L.post_norm, L.gate_up.qweight,
                                         c.intermediate, c.hidden, c.eps, residual_out=self.res_b,
                                         out=self.act)
+        elif self.batch > 1:
+            B = self.batch
+            ops.add_rmsnorm(x_in, r_in, L.input_norm, c.eps, out=self.h, residual_out=self.res_a)
+            ops.q4_0_gemm(self.h, L.qkv.qweight, c.qkv_rows, c.hidden, out=self.qkv_out)
+            ops.qknorm_rope_kv_write(self.qkv_out, L.q_norm, L.k_norm, self.cos_sin, st.positions,
+                                     st.slot_mapping, L.kv_cache[0], L.kv_cache[1], c.n_q, c.n_kv,
+                                     c.eps, q_out=self.q)
+            ops.splitkv_decode_merged(self.q, L.kv_cache[0], L.kv_cache[1], st.block_table,
+                                      st.seq_lens, self.num_splits, self.scale, self.partial_o,
+                                      self.partial_lse, out=self.attn)
+            ops.q4_0_gemm(self.attn.view(B, -1), L.o_proj.qweight, c.hidden, c.n_q * c.head_dim,
+                          out=self.o)
+            ops.add_rmsnorm(self.o, self.res_a, L.post_norm, c.eps, out=self.h2,
+                            residual_out=self.res_b)
+            ops.q4_0_gemm_swiglu(self.h2, L.gate_up.qweight, c.intermediate, c.hidden,
+                                 out=self.act)
+            ops.q4_0_gemm(self.act, L.down.qweight, c.hidden, c.intermediate, out=self.d)
+            return
         else:
             ops.add_rmsnorm(x_in, r_in, L.input_norm, c.eps, out=self.h, residual_out=self.res_a)
             ops.q4_0_gemv(self.h, L.qkv.qweight, c.qkv_rows, c.hidden, out=self.qkv_out)
@@ -260,6 +284,10 @@ class DecodeModel:
                                         c.vocab, c.hidden, c.eps, self.argmax_keys.view(-1),
                                         out=self.logits)
             keys = self.argmax_keys
+        elif self.batch > 1:
+            ops.add_rmsnorm(x_in, r_in, self.final_norm, c.eps, out=self.h)
+            ops.q4_0_gemm(self.h, self.head.q4_0_head, c.vocab, c.hidden, out=self.logits)
+            ops.argmax(self.logits, out=st.next_ids)
         else:
             ops.add_rmsnorm(x_in, r_in, self.final_norm, c.eps, out=self.h)
             ops.q4_0_gemv(self.h, self.head.q4_0_head, c.vocab, c.hidden, out=self.logits)
@@ -289,32 +317,60 @@ class DecodeModel:
             self.enqueue_step()
 
     # --------------------------------------------------------------- control
-    def reset(self, prompt: torch.Tensor) -> None:
-        """Position 0 holds prompt[0]; the advance kernel feeds the remaining
-        prompt tokens, then the model's own argmax."""
+    def reset(self, prompt) -> None:
+        """Position 0 of each sequence holds its prompt[0]; the advance kernel
+        feeds the remaining prompt tokens, then the model's own argmax.
+        prompt: a 1-D tensor (batch 1, or the same prompt for every sequence)
+        or a list of `batch` 1-D tensors (prompts of any lengths)."""
         st = self.state
-        seq = prompt.to(device=self.device, dtype=torch.int64).view(-1)
-        if not 1 <= seq.numel() <= self.max_len:
-            raise ValueError("prompt must have 1..max_len tokens")
+        B = self.batch
+        prompts = list(prompt) if isinstance(prompt, (list, tuple)) else [prompt] * B
+        if len(prompts) != B:
+            raise ValueError(f"need {B} prompts")
         st.forced.zero_()
-        st.forced[0, :seq.numel()] = seq
-        st.forced_len.fill_(seq.numel())
         st.tokens.fill_(-1)
-        st.tokens[0, 0] = seq[0]
-        st.ids.copy_(seq[:1])
+        lens = []
+        for r, p in enumerate(prompts):
+            seq = torch.as_tensor(p).to(device=self.device, dtype=torch.int64).view(-1)
+            if not 1 <= seq.numel() <= self.max_len:
+                raise ValueError("a prompt must have 1..max_len tokens")
+            st.forced[r, :seq.numel()] = seq
+            st.tokens[r, 0] = seq[0]
+            st.ids[r] = seq[0]
+            lens.append(seq.numel())
+        st.forced_len.copy_(torch.tensor(lens, dtype=torch.int32))
         st.positions.zero_()
         st.seq_lens.fill_(1)
-        st.slot_mapping.copy_(st.block_table[0, :1].to(torch.int64) * self.cfg.block_size)
+        st.slot_mapping.copy_(st.block_table[:, 0].to(torch.int64) * self.cfg.block_size)
 
-    def generate(self, prompt: torch.Tensor, new_tokens: int) -> torch.Tensor:
-        """Greedy decode: feeds the prompt, then new_tokens generated tokens.
-        Returns the token ids by position (prompt followed by generated)."""
-        n = prompt.numel()
-        total = n + new_tokens
+    def set_context(self, lengths, ids=None) -> None:
+        """Continue every sequence r at position lengths[r] (the KV cache
+        below it is whatever it holds): for timing decode at given contexts."""
+        st = self.state
+        L = torch.as_tensor(lengths, dtype=torch.int64).view(-1)
+        if L.numel() != self.batch or int(L.min()) < 0 or int(L.max()) >= self.max_len:
+            raise ValueError("one length per sequence, below max_len")
+        st.forced_len.zero_()
+        st.positions.copy_(L)
+        st.seq_lens.copy_((L + 1).to(torch.int32))
+        bs = self.cfg.block_size
+        rows = torch.arange(self.batch, device=self.device)
+        Ld = L.to(self.device)
+        st.slot_mapping.copy_(st.block_table[rows, Ld // bs].to(torch.int64) * bs + Ld % bs)
+        st.ids.copy_(torch.as_tensor(ids if ids is not None else [1] * self.batch,
+                                     dtype=torch.int64))
+
+    def generate(self, prompt, new_tokens: int) -> torch.Tensor:
+        """Greedy decode: feeds the prompt(s), then new_tokens generated
+        tokens.  Returns the token ids by position (prompt followed by
+        generated): [total] for batch 1, else [batch, longest total]."""
+        prompts = list(prompt) if isinstance(prompt, (list, tuple)) else [prompt] * self.batch
+        total = max(int(torch.as_tensor(p).numel()) for p in prompts) + new_tokens
         if total > self.max_len:
             raise ValueError("prompt + new_tokens exceeds max_len")
         self.reset(prompt)
         for _ in range(total - 1):
             self.step()
         torch.cuda.synchronize(self.device)
-        return self.state.tokens[0, :total].clone()
+        out = self.state.tokens[:, :total].clone()
+        return out[0] if self.batch == 1 else out
