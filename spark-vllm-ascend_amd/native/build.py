@@ -27,6 +27,9 @@ COMMON = [
     "-Wall",
     "-Wno-unused-function",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # leading scalar/pointer kernel arguments arrive in SGPRs (gfx950 kernarg
+    # preloading): no scalar-load round trip before a kernel's first loads
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
 ]
 SOURCES = ["q4_0_gemv.hip", "q4_0_gemm.hip", "splitkv_attention.hip", "small_ops.hip", "abi.cpp"]
 

@@ -113,6 +113,18 @@ struct GemvArgs {
   float eps;
 };
 
+// The arguments only the epilogue (and the norm) needs, passed after the
+// ones every wave needs at once: the kernel is built with kernel-argument
+// preloading, which puts the leading scalar and pointer arguments in SGPRs
+// before the first instruction (an aggregate is not preloaded), so the
+// weight and activation loads issue without waiting for a kernarg fetch.
+struct GemvTail {
+  uint16_t* residual_out;
+  uint16_t* y;
+  uint64_t* argmax_keys;
+  float eps;
+};
+
 // One workgroup owns RG groups of 8 weight rows.  Its waves split the K
 // dimension: pair group g (pairs 8g..8g+7) belongs to wave g % ks, and lane
 // 8r+c of a wave handles pair 8g+c of row r.  Each wave stages the
@@ -127,10 +139,24 @@ struct GemvArgs {
 //  EPI_ARGMAX: besides y, each workgroup writes the max (value, -index) key
 //       of its rows, for an on-device greedy argmax.
 template <int NPMAX, int RG, bool PRO, int EPI>
-__global__ __launch_bounds__(NPMAX <= 2 ? 1024 : 512) void q4_0_gemv_kernel(GemvArgs a) {
+__global__ __launch_bounds__(NPMAX <= 2 ? 1024 : 512) void q4_0_gemv_kernel(
+    const uint8_t* w_, const uint16_t* x_, const uint16_t* residual_, const uint16_t* gamma_,
+    int npairs_, int n_out_, int64_t up_offset_rows_, int ks_, GemvTail tail) {
+  GemvArgs a;
+  a.w = w_;
+  a.x = x_;
+  a.residual = residual_;
+  a.gamma = gamma_;
+  a.npairs = npairs_;
+  a.n_out = n_out_;
+  a.up_offset_rows = up_offset_rows_;
+  a.residual_out = tail.residual_out;
+  a.y = tail.y;
+  a.argmax_keys = tail.argmax_keys;
+  a.eps = tail.eps;
   extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
   constexpr bool SWIGLU = EPI == EPI_SWIGLU;
-  const int ks = blockDim.x >> 6;
+  const int ks = ks_;  // waves per workgroup (blockDim.x / 64, passed to be preloaded)
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -389,8 +415,10 @@ static hipError_t launch_fast(hipStream_t s, const GemvArgs& a, int ks) {
   constexpr int OUT_PER_WG = (EPI == EPI_SWIGLU ? 4 : 8) * RG;
   const int grid = (a.n_out + OUT_PER_WG - 1) / OUT_PER_WG;
   const size_t lds = (size_t)ks * NPMAX * 8 * 36 * 4 + (size_t)ks * 8 * RG * 4 + (size_t)ks * 4;
+  const GemvTail tail{a.residual_out, a.y, a.argmax_keys, a.eps};
   hipLaunchKernelGGL((q4_0_gemv_kernel<NPMAX, RG, PRO, EPI>), dim3(grid), dim3(64 * ks), lds, s,
-                     a);
+                     a.w, a.x, a.residual, a.gamma, a.npairs, a.n_out, a.up_offset_rows, ks,
+                     tail);
   return hipGetLastError();
 }
 

@@ -181,3 +181,13 @@ def test_partial_sentinels(ops, dev):
     go, gl = guard_o.cpu().numpy(), guard_l.cpu().numpy()
     assert np.all(go[:32] == 17) and np.all(go[-32:] == 17)
     assert np.all(gl[:32] == 17) and np.all(gl[-32:] == 17)
+
+
+@pytest.mark.parametrize("merged", [False, True])
+def test_zero_length_gives_zero_output(ops, dev, merged):
+    """Sequences with no tokens: every split is empty and the merge has no
+    weight, so the output is zero (not NaN)."""
+    rng = np.random.default_rng(9)
+    q, kc, vc, table = _case(rng, [1, 1], 128)
+    out, _, pl = _run(ops, dev, q, kc, vc, table, [0, 0], 8, HD ** -0.5, merged=merged)
+    assert np.all(out == 0)
