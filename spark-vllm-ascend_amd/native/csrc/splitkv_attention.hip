@@ -99,8 +99,25 @@ __device__ __forceinline__ void norm_rope_head(float a, float b, float ga, float
   *v_out = f32_to_bf16(bn * c + an * sn);
 }
 
+// The arguments the first loads depend on are passed ahead of the rest as
+// scalars and pointers (14 dwords): the library is built with kernel-argument
+// preloading, which places leading non-aggregate arguments in SGPRs, so the
+// first loads issue without a kernarg fetch.
 template <int WAVES, int BLK, bool FUSEQ>
-__global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(SplitKVArgs A) {
+__global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(
+    const int32_t* block_table_, const int32_t* seq_lens_, const int64_t* positions_,
+    const int64_t* slot_mapping_, const uint16_t* q_, int num_splits_, int max_blocks_,
+    int bs_log2_, int n_kv_, SplitKVArgs A) {
+  A.block_table = block_table_;
+  A.seq_lens = seq_lens_;
+  A.positions = positions_;
+  A.slot_mapping = slot_mapping_;
+  A.q = q_;
+  A.num_splits = num_splits_;
+  A.max_blocks = max_blocks_;
+  A.bs_log2 = bs_log2_;
+  A.n_kv = n_kv_;
+  A.n_q = 4 * n_kv_;  // GQA 4:1 (validated on the host)
   static_assert(BLK == 32 || BLK == 64, "blocks of 32 or 64 tokens");
   constexpr int RB = BLK / 8;  // 8-token steps per block
   const uint16_t* __restrict__ kc = A.kc;
@@ -130,20 +147,70 @@ __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(SplitKVArgs 
   const int s0 = split * tps;
   const int w0 = min(s0 + wave * wlen, cap);
   const int32_t* bt = block_table + (int64_t)seq * max_blocks;
-  const int bt0 = bt[w0 < cap ? (w0 >> bs_log2) : 0];
-  const int bt1 = bt[w0 + 32 < cap ? ((w0 + 32) >> bs_log2) : 0];
-  const int L = min(A.seq_lens[seq], cap);
+  // The wave-uniform values this workgroup starts from (length, the first
+  // two pages of the wave's chunk, position and slot) in ONE vector load,
+  // one address per lane, then v_readlane: scalar loads would each cost a
+  // full lgkmcnt(0) wait (their results return out of order), and the
+  // compiler issues them one by one next to their uses.
+  uint32_t gv;
+  {
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(A.seq_lens + seq);
+    if (lane == 1) src = reinterpret_cast<const uint32_t*>(bt + (w0 < cap ? (w0 >> bs_log2) : 0));
+    if (lane == 2)
+      src = reinterpret_cast<const uint32_t*>(bt + (w0 + 32 < cap ? ((w0 + 32) >> bs_log2) : 0));
+    if constexpr (FUSEQ) {
+      if (lane == 3 || lane == 4)
+        src = reinterpret_cast<const uint32_t*>(A.positions + seq) + (lane - 3);
+      if (lane == 5 || lane == 6)
+        src = reinterpret_cast<const uint32_t*>(A.slot_mapping + seq) + (lane - 5);
+    }
+    gv = *src;
+  }
+  // FUSEQ: this workgroup's q heads and the new token's k/v from the raw QKV
+  // row, issued in the same round trip (their addresses need nothing loaded).
+  constexpr int HPW = (G + WAVES - 1) / WAVES;  // q heads per wave (FUSEQ)
+  float qa[HPW], qb[HPW], qga = 0.f, qgb = 0.f, c = 0.f, sn = 0.f;
+  float ka = 0.f, kb = 0.f, kga = 0.f, kgb = 0.f;
+  uint16_t va = 0, vb = 0;
+  const int nh = n_q + 2 * n_kv;
+  const uint16_t* row = A.q + (int64_t)seq * nh * HD;
+  if constexpr (FUSEQ) {
+#pragma unroll
+    for (int i = 0; i < HPW; ++i) {
+      const int h = min(wave + i * WAVES, G - 1);
+      qa[i] = bf16_bits_to_f32(row[(kvh * G + h) * HD + lane]);
+      qb[i] = bf16_bits_to_f32(row[(kvh * G + h) * HD + 64 + lane]);
+    }
+    // the new token's k/v inputs (used by the owner's wave G % WAVES only)
+    ka = bf16_bits_to_f32(row[(n_q + kvh) * HD + lane]);
+    kb = bf16_bits_to_f32(row[(n_q + kvh) * HD + 64 + lane]);
+    va = row[(n_q + n_kv + kvh) * HD + lane];
+    vb = row[(n_q + n_kv + kvh) * HD + 64 + lane];
+    qga = bf16_bits_to_f32(A.q_gamma[lane]);
+    qgb = bf16_bits_to_f32(A.q_gamma[lane + 64]);
+    kga = bf16_bits_to_f32(A.k_gamma[lane]);
+    kgb = bf16_bits_to_f32(A.k_gamma[lane + 64]);
+  }
+  // Keep the scheduler from sinking those loads below the first use of the
+  // gathered values (which waits for the gather): an empty asm that clobbers
+  // memory orders the loads before it and emits no wait.
+  __asm__ volatile("" ::: "memory");
+  auto lane_u32 = [&](int l) -> uint32_t {
+    return (uint32_t)__builtin_amdgcn_readlane((int)gv, l);
+  };
+  const int bt0 = (int)lane_u32(1);
+  const int bt1 = (int)lane_u32(2);
+  const int L = min((int)lane_u32(0), cap);
   int64_t pos = 0;
-  if constexpr (FUSEQ) pos = A.positions[seq];
+  if constexpr (FUSEQ) pos = (int64_t)(((uint64_t)lane_u32(4) << 32) | lane_u32(3));
   const int s1 = min(L, s0 + tps);
   float* po = part_o + (((int64_t)seq * num_splits + split) * n_q + kvh * G) * HD;
   float* pl = part_lse + ((int64_t)seq * num_splits + split) * n_q + kvh * G;
-  if (s0 >= s1) {  // empty split (uniform over the workgroup)
-    for (int i = tid; i < G * HD; i += NT) po[i] = 0.f;
-    if (tid < G) pl[tid] = -INFINITY;
-    return;
-  }
-  const int w1 = min(s1, w0 + wlen);
+  // An empty split (no token below the length) runs the same straight-line
+  // code with no tokens and leaves (0, -inf).  It does not return early: a
+  // branch on the length, which arrives from memory, would make the compiler
+  // sink the page, position and q loads behind it, a second round trip.
+  const int w1 = s0 < s1 ? min(s1, w0 + wlen) : w0;
 
   const int bs = 1 << bs_log2;
   const int64_t tok_stride = (int64_t)n_kv * HD;
@@ -155,9 +222,10 @@ __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(SplitKVArgs 
 
   // A block-table entry outside [0, num_blocks) is never dereferenced: the
   // page is replaced by page 0 and the partial is poisoned with NaN below.
-  // A wave without tokens still issues its first block's loads (from valid
-  // pages, results unused): loads under a branch would make the compiler
-  // wait for every outstanding load before the q prologue.
+  // A wave without tokens still issues its first block's loads, all from the
+  // first row of page 0 (cached after the first touch, results unused):
+  // loads under a branch would make the compiler wait for every outstanding
+  // load before the q prologue.
   const bool has_work = w0 < w1;
   bool bad_page = false;
   auto half_base = [&](int t, int pg) -> int64_t {  // first token of a 32-token half
@@ -165,6 +233,7 @@ __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(SplitKVArgs 
       bad_page = bad_page || has_work;
       pg = 0;
     }
+    if (!has_work) pg = t = 0;
     return (int64_t)pg * page_stride + (int64_t)(t & (bs - 1)) * tok_stride + kvh * HD;
   };
   // Every K and V load of one 64-token block; tokens past the chunk end are
@@ -192,41 +261,19 @@ __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(SplitKVArgs 
       for (int hf = 0; hf < 2; ++hf)
         vr[jp][hf] = reinterpret_cast<const u32x4*>(vc + tok_off(8 * jp + vt + 4 * hf))[dv];
   };
-  // The q prologue's inputs are loaded first and the first K/V block right
-  // after, so the prologue (and, fused, the q/k norm + RoPE + KV write) runs
-  // while the K/V block is in flight.
-  constexpr int HPW = (G + WAVES - 1) / WAVES;  // q heads per wave (FUSEQ)
+  // The rotary row (its address needs the position) and the first K/V block
+  // (its pages) follow in the second round trip; the q/k norm + RoPE + KV
+  // write run while the K/V block is in flight.
   __shared__ __attribute__((aligned(16))) uint32_t kv_new[2][HD / 2];
   bool owner = false;
-  float qa[HPW], qb[HPW], qga = 0.f, qgb = 0.f, c = 0.f, sn = 0.f;
-  float ka = 0.f, kb = 0.f, kga = 0.f, kgb = 0.f;
-  uint16_t va = 0, vb = 0;
   int64_t slot = -1;
-  const int nh = n_q + 2 * n_kv;
-  const uint16_t* row = A.q + (int64_t)seq * nh * HD;
   u32x4 qv = u32x4{0u, 0u, 0u, 0u};
   if constexpr (FUSEQ) {
     owner = pos >= s0 && pos < s0 + tps && pos < L;
     const int64_t pc = pos < 0 ? 0 : (pos >= A.max_position ? A.max_position - 1 : pos);
-#pragma unroll
-    for (int i = 0; i < HPW; ++i) {
-      const int h = min(wave + i * WAVES, G - 1);
-      qa[i] = bf16_bits_to_f32(row[(kvh * G + h) * HD + lane]);
-      qb[i] = bf16_bits_to_f32(row[(kvh * G + h) * HD + 64 + lane]);
-    }
-    qga = bf16_bits_to_f32(A.q_gamma[lane]);
-    qgb = bf16_bits_to_f32(A.q_gamma[lane + 64]);
     c = bf16_bits_to_f32(A.cos_sin[pc * HD + lane]);
     sn = bf16_bits_to_f32(A.cos_sin[pc * HD + 64 + lane]);
-    {  // the new token's k/v inputs (used by the owner's wave G % WAVES only)
-      ka = bf16_bits_to_f32(row[(n_q + kvh) * HD + lane]);
-      kb = bf16_bits_to_f32(row[(n_q + kvh) * HD + 64 + lane]);
-      kga = bf16_bits_to_f32(A.k_gamma[lane]);
-      kgb = bf16_bits_to_f32(A.k_gamma[lane + 64]);
-      va = row[(n_q + n_kv + kvh) * HD + lane];
-      vb = row[(n_q + n_kv + kvh) * HD + 64 + lane];
-      slot = A.slot_mapping[seq];
-    }
+    slot = (int64_t)(((uint64_t)lane_u32(6) << 32) | lane_u32(5));
   } else {
     qv = reinterpret_cast<const u32x4*>(A.q + ((int64_t)seq * n_q + kvh * G) * HD)[lane];
   }
@@ -418,8 +465,11 @@ __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(SplitKVArgs 
       lt += a * l_w[wv][h];
       ot += a * o_w[wv][e];
     }
-    po[e] = bad ? __builtin_nanf("") : ot / lt;
-    if ((e % HD) == 0) pl[h] = bad ? __builtin_nanf("") : (mt + log2f(lt)) * 0.69314718055994530942f;
+    // lt == 0 only when the split has no token: the empty partial (0, -inf)
+    po[e] = bad ? __builtin_nanf("") : (lt > 0.f ? ot / lt : 0.f);
+    if ((e % HD) == 0)
+      pl[h] = bad ? __builtin_nanf("")
+                  : (lt > 0.f ? (mt + log2f(lt)) * 0.69314718055994530942f : -INFINITY);
   }
 }
 
@@ -518,7 +568,8 @@ int launch_splitkv(void* stream, smx::SplitKVArgs a, int32_t num_seqs, int32_t b
   const dim3 grid(a.num_splits, a.n_kv, num_seqs);
 #define SMX_ATTN_LAUNCH(W, B)                                                                   \
   hipLaunchKernelGGL((smx::splitkv_decode_kernel<W, B, FUSEQ>), grid, dim3(64 * W), 0,          \
-                     (hipStream_t)stream, a)
+                     (hipStream_t)stream, a.block_table, a.seq_lens, a.positions,                  \
+                     a.slot_mapping, a.q, a.num_splits, a.max_blocks, a.bs_log2, a.n_kv, a)
   if (blk == 32) {
     if (waves == 8) SMX_ATTN_LAUNCH(8, 32);
     else if (waves == 4) SMX_ATTN_LAUNCH(4, 32);
