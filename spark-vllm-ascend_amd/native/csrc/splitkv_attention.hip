@@ -473,70 +473,71 @@ __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(
   }
 }
 
-// Log-sum-exp merge: one workgroup of 256 threads per (q head, sequence);
-// thread (half, d) folds the splits of its half with an online max, so every
-// load it needs (its partial values and the lse values, up to MB of each)
-// is issued at once; the two halves meet in LDS.
-__global__ __launch_bounds__(256) void lse_merge_kernel(const float* __restrict__ part_o,
-                                                        const float* __restrict__ part_lse,
-                                                        uint16_t* __restrict__ out,
-                                                        int num_splits, int n_q) {
-  constexpr int MB = 32;
-  __shared__ float xm[HD], xl[HD], xa[HD];
-  const int h = blockIdx.x, seq = blockIdx.y;
-  const int d = threadIdx.x & (HD - 1), half = threadIdx.x >> 7;
-  const int per = (num_splits + 1) / 2;
-  const int sb = half * per, se = min(num_splits, sb + per);
-  const float* lse = part_lse + (int64_t)seq * num_splits * n_q + h;
-  const int64_t stride = (int64_t)n_q * HD;
-  const float* src = part_o + ((int64_t)seq * num_splits * n_q + h) * HD + d;
+// Max / sum over the 64 lanes of a wave (every lane gets the result).
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp_f32<DPP_QUAD_XOR1>(v));
+  v = fmaxf(v, dpp_f32<DPP_QUAD_XOR2>(v));
+  v = fmaxf(v, dpp_f32<DPP_ROW_HALF_MIRROR>(v));
+  v = fmaxf(v, dpp_f32<DPP_ROW_MIRROR>(v));
+  v = fmaxf(v, shfl_xor_f32(v, 16));
+  v = fmaxf(v, shfl_xor_f32(v, 32));
+  return v;
+}
+
+// Log-sum-exp merge (merge_attention, src/spark_vllm_ascend/kernels/
+// vector.py:61-78): w_s = exp(lse_s - max), out = sum_s w_s o_s / sum_s w_s.
+// One wave per (64 dims of a q head, sequence), splits in chunks of 64:
+// lane j loads the lse of split j (one vector load), the chunk's max and the
+// weight sum are wave reductions and each lane computes one weight; lane d
+// then folds the chunk's partials of its dim with the weights broadcast
+// from their lanes (v_readlane).  Every load of a chunk is unconditional
+// (indices past the last split are clamped, with uniform scalar arithmetic,
+// and carry no weight), so a chunk costs one round trip.  Splits with
+// lse = -inf carry no weight; a NaN lse or partial makes the output NaN; no
+// weight at all gives 0.
+__global__ __launch_bounds__(64) void lse_merge_kernel(const float* __restrict__ part_o,
+                                                       const float* __restrict__ part_lse,
+                                                       uint16_t* __restrict__ out,
+                                                       int num_splits, int n_q) {
+  const int h = blockIdx.x >> 1, seq = blockIdx.y;
+  const int lane = threadIdx.x, d = (blockIdx.x & 1) * 64 + lane;
+  const int64_t row = (int64_t)seq * num_splits * n_q + h;  // (seq, split 0, h)
+  const int pstep = n_q * HD;  // n_q <= 65535: 63 steps stay below 2^31
   float m = -INFINITY, l = 0.f, acc = 0.f;
-  bool poisoned = false;  // a NaN partial (e.g. a bad block-table entry) poisons the output
-  for (int b0 = sb; b0 < se; b0 += MB) {
-    float lv[MB], pv[MB];
+  bool poisoned = false;
+  for (int c0 = 0; c0 < num_splits; c0 += 64) {
+    const int last = num_splits - 1 - c0;  // last valid j of this chunk (uniform)
+    const float lraw = part_lse[row + (int64_t)(c0 + min(lane, last)) * n_q];
+    float pv[64];
+    const float* pp = part_o + (row + (int64_t)c0 * n_q) * HD + d;
+    int off = 0;  // element offset of split c0 + min(j, last): stops at the last split
 #pragma unroll
-    for (int j = 0; j < MB; ++j) {
-      const bool ok = b0 + j < se;
-      lv[j] = ok ? lse[(int64_t)(b0 + j) * n_q] : -INFINITY;
-      pv[j] = ok ? src[(b0 + j) * stride] : 0.f;
+    for (int j = 0; j < 64; ++j) {
+      pv[j] = pp[off];
+      off += j < last ? pstep : 0;
     }
-    float mb = m;
+    // every load of the chunk is issued before the wait for its lse values
+    // (nothing may be scheduled across this point)
+    __builtin_amdgcn_sched_barrier(0);
+    const float lv = lane <= last ? lraw : -INFINITY;
+    poisoned |= __builtin_amdgcn_ballot_w64(lv != lv) != 0;
+    // Branch-free (a branch would let the compiler sink the partial loads
+    // behind the lse wait): with no weight so far both factors are 0.
+    const float mc = fmaxf(m, wave_max(lv));
+    const float wl = lv == -INFINITY ? 0.f : expf(lv - mc);
+    const float a = m == -INFINITY ? 0.f : expf(m - mc);
+    l = l * a + wave_sum(wl);
+    acc *= a;
 #pragma unroll
-    for (int j = 0; j < MB; ++j) {
-      poisoned |= lv[j] != lv[j];
-      mb = fmaxf(mb, lv[j]);
+    for (int j = 0; j < 64; ++j) {
+      const float wj = __builtin_bit_cast(
+          float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), j));
+      acc = fmaf(wj, pv[j], acc);
     }
-    if (mb != -INFINITY) {
-      const float a = expf(m - mb);
-      l *= a;
-      acc *= a;
-#pragma unroll
-      for (int j = 0; j < MB; ++j) {
-        const float wj = lv[j] == -INFINITY ? 0.f : expf(lv[j] - mb);
-        l += wj;
-        acc += wj * pv[j];
-      }
-      m = mb;
-    }
+    m = mc;
   }
-  if (poisoned) acc = __builtin_nanf("");
-  if (half == 1) {
-    xm[d] = m;
-    xl[d] = l;
-    xa[d] = acc;
-  }
-  __syncthreads();
-  if (half == 0) {
-    const float m2 = xm[d], l2 = xl[d], a2 = xa[d];
-    const float mt = fmaxf(m, m2);
-    const float f1 = m == -INFINITY ? 0.f : expf(m - mt);
-    const float f2 = m2 == -INFINITY ? 0.f : expf(m2 - mt);
-    const float lt = l * f1 + l2 * f2;
-    const float at = acc * f1 + a2 * f2;
-    const bool nan_in = acc != acc || a2 != a2;
-    out[((int64_t)seq * n_q + h) * HD + d] =
-        f32_to_bf16(nan_in ? __builtin_nanf("") : (lt > 0.f ? at / lt : 0.f));
-  }
+  const float v = poisoned || acc != acc ? __builtin_nanf("") : (l > 0.f ? acc / l : 0.f);
+  out[((int64_t)seq * n_q + h) * HD + d] = f32_to_bf16(v);
 }
 
 }  // namespace
@@ -610,7 +611,7 @@ smx::SplitKVArgs splitkv_args(const void* q, const void* k_cache, const void* v_
 
 int launch_merge(void* stream, const float* partial_o, const float* partial_lse, void* out,
                  int32_t num_seqs, int32_t num_splits, int32_t n_q) {
-  hipLaunchKernelGGL(smx::lse_merge_kernel, dim3(n_q, num_seqs), dim3(256), 0,
+  hipLaunchKernelGGL(smx::lse_merge_kernel, dim3(2 * n_q, num_seqs), dim3(64), 0,
                      (hipStream_t)stream, partial_o, partial_lse, (uint16_t*)out, num_splits,
                      n_q);
   return (int)hipGetLastError();
