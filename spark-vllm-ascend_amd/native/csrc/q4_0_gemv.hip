@@ -444,7 +444,12 @@ static GemvShape pick_shape(int n_out, int out_per_group, int ngroups, bool norm
     sh.np = (ngroups + 7) / 8;
     sh.ks = (ngroups + sh.np - 1) / sh.np;
   }
-  const char* e = getenv("SMX_GEMV_SHAPE");  // "rg,ks" override for tuning sweeps
+  // "rg,ks" overrides for tuning sweeps: SMX_GEMV_SHAPE_<n_out>_<ngroups> for
+  // one shape, else SMX_GEMV_SHAPE for every shape.
+  char key[64];
+  snprintf(key, sizeof(key), "SMX_GEMV_SHAPE_%d_%d", n_out, ngroups);
+  const char* e = getenv(key);
+  if (!e) e = getenv("SMX_GEMV_SHAPE");
   if (e) {
     int a = 0, b = 0;
     if (sscanf(e, "%d,%d", &a, &b) == 2 && (a == 1 || a == 2 || a == 4) && b >= 1 && b <= 16) {

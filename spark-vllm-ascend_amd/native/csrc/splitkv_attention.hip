@@ -102,16 +102,23 @@ __device__ __forceinline__ void norm_rope_head(float a, float b, float ga, float
 // The arguments the first loads depend on are passed ahead of the rest as
 // scalars and pointers (14 dwords): the library is built with kernel-argument
 // preloading, which places leading non-aggregate arguments in SGPRs, so the
-// first loads issue without a kernarg fetch.
+// first loads issue without a kernarg fetch.  pa_ / pb_ are the positions
+// and slots (FUSEQ: the per-sequence gather reads them at entry) or the K and
+// V caches (plain: read as soon as the first pages are known).
 template <int WAVES, int BLK, bool FUSEQ>
 __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(
-    const int32_t* block_table_, const int32_t* seq_lens_, const int64_t* positions_,
-    const int64_t* slot_mapping_, const uint16_t* q_, int num_splits_, int max_blocks_,
-    int bs_log2_, int n_kv_, SplitKVArgs A) {
+    const int32_t* block_table_, const int32_t* seq_lens_, const void* pa_, const void* pb_,
+    const uint16_t* q_, int num_splits_, int max_blocks_, int bs_log2_, int n_kv_,
+    SplitKVArgs A) {
   A.block_table = block_table_;
   A.seq_lens = seq_lens_;
-  A.positions = positions_;
-  A.slot_mapping = slot_mapping_;
+  if constexpr (FUSEQ) {
+    A.positions = (const int64_t*)pa_;
+    A.slot_mapping = (const int64_t*)pb_;
+  } else {
+    A.kc = (const uint16_t*)pa_;
+    A.vc = (const uint16_t*)pb_;
+  }
   A.q = q_;
   A.num_splits = num_splits_;
   A.max_blocks = max_blocks_;
@@ -206,11 +213,15 @@ __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(
   const int s1 = min(L, s0 + tps);
   float* po = part_o + (((int64_t)seq * num_splits + split) * n_q + kvh * G) * HD;
   float* pl = part_lse + ((int64_t)seq * num_splits + split) * n_q + kvh * G;
-  // An empty split (no token below the length) runs the same straight-line
-  // code with no tokens and leaves (0, -inf).  It does not return early: a
-  // branch on the length, which arrives from memory, would make the compiler
-  // sink the page, position and q loads behind it, a second round trip.
-  const int w1 = s0 < s1 ? min(s1, w0 + wlen) : w0;
+  // An empty split (no token below the length) leaves (0, -inf).  Its exit
+  // comes only now, after the gathered values arrived: the loads above are
+  // already in flight, so the branch costs no round trip.
+  if (s0 >= s1) {  // uniform over the workgroup
+    for (int i = tid; i < G * HD; i += NT) po[i] = 0.f;
+    if (tid < G) pl[tid] = -INFINITY;
+    return;
+  }
+  const int w1 = min(s1, w0 + wlen);
 
   const int bs = 1 << bs_log2;
   const int64_t tok_stride = (int64_t)n_kv * HD;
@@ -569,8 +580,10 @@ int launch_splitkv(void* stream, smx::SplitKVArgs a, int32_t num_seqs, int32_t b
   const dim3 grid(a.num_splits, a.n_kv, num_seqs);
 #define SMX_ATTN_LAUNCH(W, B)                                                                   \
   hipLaunchKernelGGL((smx::splitkv_decode_kernel<W, B, FUSEQ>), grid, dim3(64 * W), 0,          \
-                     (hipStream_t)stream, a.block_table, a.seq_lens, a.positions,                  \
-                     a.slot_mapping, a.q, a.num_splits, a.max_blocks, a.bs_log2, a.n_kv, a)
+                     (hipStream_t)stream, a.block_table, a.seq_lens,                               \
+                     FUSEQ ? (const void*)a.positions : (const void*)a.kc,                         \
+                     FUSEQ ? (const void*)a.slot_mapping : (const void*)a.vc, a.q, a.num_splits,   \
+                     a.max_blocks, a.bs_log2, a.n_kv, a)
   if (blk == 32) {
     if (waves == 8) SMX_ATTN_LAUNCH(8, 32);
     else if (waves == 4) SMX_ATTN_LAUNCH(4, 32);
