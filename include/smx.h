@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define SMX_ABI_VERSION 1
+#define SMX_ABI_VERSION 2
 
 /* Return codes besides 0 and hipError_t values. */
 #define SMX_EINVAL 10001      /* an argument failed validation */
@@ -321,7 +321,11 @@ int smx_reshape_and_cache(void* stream, const void* key, const void* value,
  *   positions[r] = p; seq_lens[r] = p + 1;
  *   slot_mapping[r] = block_table[r, p / block_size] * block_size
  *                     + p % block_size  (-1 when the table has no entry);
- *   tokens_out[r, p] = ids[r] when tokens_out != NULL and p < max_len.
+ *   tokens_out[r, p] = ids[r] when tokens_out != NULL and p < max_len;
+ *   embed_out[r, :] = embed_table[ids[r], :] when embed_table != NULL
+ *       (embed_table [vocab, hidden] bf16, zeros for an id outside [0, vocab)):
+ *       the next step's embedding gather, done here instead of by a launch of
+ *       its own (smx_embedding).
  * forced_ids is [rows, max_len] and forced_len an int32 [rows] device array
  * (both NULL when no tokens are forced); keeping the forced length in device
  * memory lets one graph switch from prompt to generated tokens.  The slot
@@ -334,7 +338,9 @@ int smx_decode_advance(void* stream, int64_t* next_ids,
                        int64_t* ids, int64_t* positions, int32_t* seq_lens,
                        int64_t* slot_mapping, const int32_t* block_table,
                        int64_t* tokens_out, int32_t rows, int32_t max_blocks,
-                       int32_t block_size, int32_t max_len);
+                       int32_t block_size, int32_t max_len,
+                       const void* embed_table, void* embed_out, int64_t vocab,
+                       int64_t hidden);
 
 #ifdef __cplusplus
 }

@@ -10,7 +10,6 @@ one device graph (src/tools/deployment/serve.py:34).
 
 Here one decode step is the kernel sequence (fused=True, the default)
 
-  embedding
   per layer:  add + RMSNorm(input_norm) fused into the QKV Q4_0 GEMV
               -> q/k RMSNorm + RoPE + KV write fused into split-KV attention
               -> LSE merge -> o_proj Q4_0 GEMV
@@ -18,7 +17,8 @@ Here one decode step is the kernel sequence (fused=True, the default)
                  Q4_0 GEMV with SwiGLU -> down Q4_0 GEMV
   add + RMSNorm(final norm) fused into the head Q4_0 GEMV, whose workgroups
   also leave per-workgroup argmax keys -> on-device advance (reduces the keys
-  to the next input id; position, sequence length, KV slot)
+  to the next input id; position, sequence length, KV slot; gathers the next
+  id's embedding row, the input of the next step)
 
 i.e. 6 launches per layer.  Each layer hands (down output, residual) to the
 next, whose first GEMV adds and normalises them (the reference's "next norm"
@@ -274,7 +274,8 @@ class DecodeModel:
     def enqueue_step(self) -> None:
         c, st = self.cfg, self.state
         ops = torch_ops
-        self.head.embed(st.ids, out=self.x)
+        # self.x holds the embedding of st.ids: gathered by the previous
+        # step's advance kernel, or by reset() / set_context()
         for i in range(len(self.layers)):
             self.layer_run(i)
         x_in, r_in = self._layer_input(len(self.layers))
@@ -294,7 +295,8 @@ class DecodeModel:
             ops.argmax(self.logits, out=st.next_ids)
         ops.decode_advance(st.next_ids, st.ids, st.positions, st.seq_lens, st.slot_mapping,
                            st.block_table, c.block_size, tokens_out=st.tokens,
-                           forced_ids=st.forced, forced_len=st.forced_len, argmax_keys=keys)
+                           forced_ids=st.forced, forced_len=st.forced_len, argmax_keys=keys,
+                           embed_table=self.head.weight, embed_out=self.x)
 
     def capture(self) -> None:
         """Capture one decode step as a graph.  Clobbers the decode state;
@@ -342,6 +344,7 @@ class DecodeModel:
         st.positions.zero_()
         st.seq_lens.fill_(1)
         st.slot_mapping.copy_(st.block_table[:, 0].to(torch.int64) * self.cfg.block_size)
+        self.head.embed(st.ids, out=self.x)
 
     def set_context(self, lengths, ids=None) -> None:
         """Continue every sequence r at position lengths[r] (the KV cache
@@ -359,6 +362,7 @@ class DecodeModel:
         st.slot_mapping.copy_(st.block_table[rows, Ld // bs].to(torch.int64) * bs + Ld % bs)
         st.ids.copy_(torch.as_tensor(ids if ids is not None else [1] * self.batch,
                                      dtype=torch.int64))
+        self.head.embed(st.ids, out=self.x)
 
     def generate(self, prompt, new_tokens: int) -> torch.Tensor:
         """Greedy decode: feeds the prompt(s), then new_tokens generated

@@ -16,7 +16,7 @@ import ctypes
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libsmx.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 SMX_EINVAL = 10001
 SMX_EUNSUPPORTED = 10002
 
@@ -50,7 +50,7 @@ SIGNATURES = {
     "smx_argmax_bf16": [_P, _P, _I64, _I64, _P],
     "smx_reshape_and_cache": [_P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32],
     "smx_decode_advance": [_P, _P, _P, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32,
-                           _I32],
+                           _I32, _P, _P, _I64, _I64],
     "smx_q4_0_add_rmsnorm_gemv": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _F32],
     "smx_q4_0_add_rmsnorm_gemv_swiglu": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _F32],
     "smx_q4_0_add_rmsnorm_gemv_argmax": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _F32],

@@ -208,44 +208,83 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const uint16_t* __restrict
 // One workgroup of 1024 threads per row.  With argmax_keys, the row's next
 // token is first reduced from the per-workgroup keys of the head GEMV
 // (max value, then lowest index) and stored to next_ids.
+// One 1024-thread workgroup per row, in three round trips of loads:
+//  1. every thread loads 16 argmax keys at once (indices clamped to the last
+//     key: a repeated key does not change a maximum), thread 0 the row's
+//     position, forced length and (without keys) next id;
+//  2. thread 0 loads the forced token and the block-table entry of the new
+//     position (clamped indices, selected afterwards) while the keys reduce;
+//  3. with embed_table, every thread gathers its share of the new token's
+//     embedding row for the next step (zeros for an id outside the vocab).
 __global__ __launch_bounds__(1024) void decode_advance_kernel(
     int64_t* __restrict__ next_ids, const uint64_t* __restrict__ argmax_keys, int num_keys,
     const int64_t* __restrict__ forced_ids, const int32_t* __restrict__ forced_len,
     int64_t* ids, int64_t* positions, int32_t* seq_lens, int64_t* slot_mapping,
     const int32_t* block_table, int64_t* tokens_out, int max_blocks, int block_size,
-    int max_len) {
+    int max_len, const uint16_t* __restrict__ embed_table, uint16_t* __restrict__ embed_out,
+    int64_t vocab, int64_t hidden) {
+  constexpr int KPT = 16;  // keys per thread per round trip
   __shared__ uint64_t red[16];
-  const int r = blockIdx.x;
+  __shared__ int64_t s_nid;
+  const int r = blockIdx.x, tid = threadIdx.x;
+  int64_t pos0 = 0, nxt0 = 0;
+  int flen = 0;
+  if (tid == 0) {
+    pos0 = positions[r];
+    if (forced_ids) flen = forced_len[r];
+    if (!argmax_keys) nxt0 = next_ids[r];
+  }
+  uint64_t key = 0;
   if (argmax_keys) {
-    uint64_t key = 0;
     const uint64_t* kr = argmax_keys + (int64_t)r * num_keys;
-    for (int i = threadIdx.x; i < num_keys; i += blockDim.x) key = kr[i] > key ? kr[i] : key;
+    for (int c0 = 0; c0 < num_keys; c0 += 1024 * KPT) {
+      uint64_t kv[KPT];
+#pragma unroll
+      for (int j = 0; j < KPT; ++j) kv[j] = kr[min(c0 + j * 1024 + tid, num_keys - 1)];
+#pragma unroll
+      for (int j = 0; j < KPT; ++j) key = kv[j] > key ? kv[j] : key;
+    }
+  }
+  int64_t p = 0, fid = 0;
+  int32_t bte = 0;
+  if (tid == 0) {
+    p = pos0 + 1;
+    if (forced_ids) fid = forced_ids[(int64_t)r * max_len + min(p, (int64_t)max_len - 1)];
+    bte = block_table[(int64_t)r * max_blocks + min(p / block_size, (int64_t)max_blocks - 1)];
+  }
+  if (argmax_keys) {
     for (int m = 1; m < 64; m <<= 1) {
       const uint64_t o = ((uint64_t)(uint32_t)__shfl_xor((int)(key >> 32), m, 64) << 32) |
                          (uint32_t)__shfl_xor((int)(uint32_t)key, m, 64);
       key = o > key ? o : key;
     }
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = key;
+    if ((tid & 63) == 0) red[tid >> 6] = key;
     __syncthreads();
-    if (threadIdx.x == 0) {
-      for (int i = 1; i < (int)(blockDim.x >> 6); ++i) key = red[i] > key ? red[i] : key;
-      next_ids[r] = key ? (int64_t)(0xffffffffu - (uint32_t)key) : 0;
-    }
   }
-  if (threadIdx.x != 0) return;
-  const int64_t p = positions[r] + 1;
-  const int64_t nid = (forced_ids && p < forced_len[r] && p < max_len)
-                          ? forced_ids[(int64_t)r * max_len + p]
-                          : next_ids[r];
-  ids[r] = nid;
-  positions[r] = p;
-  seq_lens[r] = (int32_t)(p + 1);
-  const int64_t blk = p / block_size;
-  slot_mapping[r] =
-      blk < max_blocks ? (int64_t)block_table[(int64_t)r * max_blocks + blk] * block_size +
-                             p % block_size
-                       : -1;
-  if (tokens_out && p < max_len) tokens_out[(int64_t)r * max_len + p] = nid;
+  if (tid == 0) {
+    int64_t argmax_id = nxt0;
+    if (argmax_keys) {
+      for (int i = 1; i < (int)(blockDim.x >> 6); ++i) key = red[i] > key ? red[i] : key;
+      argmax_id = key ? (int64_t)(0xffffffffu - (uint32_t)key) : 0;
+      next_ids[r] = argmax_id;
+    }
+    const int64_t nid = (forced_ids && p < flen && p < max_len) ? fid : argmax_id;
+    ids[r] = nid;
+    positions[r] = p;
+    seq_lens[r] = (int32_t)(p + 1);
+    slot_mapping[r] =
+        p / block_size < max_blocks ? (int64_t)bte * block_size + p % block_size : -1;
+    if (tokens_out && p < max_len) tokens_out[(int64_t)r * max_len + p] = nid;
+    s_nid = nid;
+  }
+  if (embed_table) {
+    __syncthreads();
+    const int64_t nid = s_nid;
+    const bool ok = nid >= 0 && nid < vocab;
+    const uint16_t* src = embed_table + (ok ? nid : 0) * hidden;
+    for (int64_t i = tid; i < hidden; i += blockDim.x)
+      embed_out[(int64_t)r * hidden + i] = ok ? src[i] : (uint16_t)0;
+  }
 }
 
 // One wave per (kv head, token): copies head_dim bf16 of K and of V.
@@ -397,7 +436,9 @@ extern "C" int smx_decode_advance(void* stream, int64_t* next_ids, const uint64_
                                   const int32_t* forced_len, int64_t* ids, int64_t* positions,
                                   int32_t* seq_lens, int64_t* slot_mapping,
                                   const int32_t* block_table, int64_t* tokens_out, int32_t rows,
-                                  int32_t max_blocks, int32_t block_size, int32_t max_len) {
+                                  int32_t max_blocks, int32_t block_size, int32_t max_len,
+                                  const void* embed_table, void* embed_out, int64_t vocab,
+                                  int64_t hidden) {
   SMX_REQUIRE(next_ids && ids && positions && seq_lens && slot_mapping && block_table,
               "null pointer argument");
   SMX_REQUIRE(rows >= 1 && rows <= 65535 && max_blocks >= 1 && block_size >= 1 && max_len >= 0,
@@ -407,13 +448,18 @@ extern "C" int smx_decode_advance(void* stream, int64_t* next_ids, const uint64_
   SMX_REQUIRE(!forced_ids || max_len >= 1, "forced_ids needs max_len >= 1");
   SMX_REQUIRE(!argmax_keys || num_keys >= 1, "argmax_keys needs num_keys >= 1");
   SMX_REQUIRE((uintptr_t)argmax_keys % 8 == 0, "argmax_keys must be 8-byte aligned");
-  hipLaunchKernelGGL(smx::decode_advance_kernel, dim3(rows), dim3(argmax_keys ? 1024 : 64), 0,
-                     (hipStream_t)stream, next_ids, argmax_keys, num_keys, forced_ids, forced_len,
-                     ids, positions, seq_lens, slot_mapping, block_table, tokens_out, max_blocks,
-                     block_size, max_len);
+  SMX_REQUIRE((embed_table == nullptr) == (embed_out == nullptr),
+              "embed_table and embed_out go together");
+  SMX_REQUIRE(!embed_table || (vocab >= 1 && hidden >= 1 && (uintptr_t)embed_table % 2 == 0 &&
+                               (uintptr_t)embed_out % 2 == 0),
+              "embedding needs vocab, hidden >= 1 and 2-byte aligned tables");
+  hipLaunchKernelGGL(smx::decode_advance_kernel, dim3(rows),
+                     dim3(argmax_keys || embed_table ? 1024 : 64), 0, (hipStream_t)stream,
+                     next_ids, argmax_keys, num_keys, forced_ids, forced_len, ids, positions,
+                     seq_lens, slot_mapping, block_table, tokens_out, max_blocks, block_size,
+                     max_len, (const uint16_t*)embed_table, (uint16_t*)embed_out, vocab, hidden);
   return (int)hipGetLastError();
 }
-
 extern "C" int smx_compute_slot_mapping(void* stream, const int32_t* query_start_loc,
                                         int32_t num_reqs, const int64_t* positions,
                                         const int32_t* block_table, int64_t* slot_mapping,

@@ -255,11 +255,14 @@ def decode_advance(next_ids: torch.Tensor, ids: torch.Tensor, positions: torch.T
                    block_size: int, tokens_out: torch.Tensor | None = None,
                    forced_ids: torch.Tensor | None = None,
                    forced_len: torch.Tensor | None = None,
-                   argmax_keys: torch.Tensor | None = None) -> None:
+                   argmax_keys: torch.Tensor | None = None,
+                   embed_table: torch.Tensor | None = None,
+                   embed_out: torch.Tensor | None = None) -> None:
     """forced_ids [rows, max_len] int64 with forced_len [rows] int32 on the
     device; tokens_out [rows, max_len] int64 (same max_len); argmax_keys
     [rows, num_keys] int64 from add_rmsnorm_gemv_argmax (next_ids is then
-    written with the argmax)."""
+    written with the argmax); embed_table [vocab, hidden] bf16 with embed_out
+    [rows, hidden]: the embedding rows of the new ids for the next step."""
     rows = ids.numel()
     _check(next_ids, "next_ids", torch.int64, rows)
     _check(ids, "ids", torch.int64, rows, next_ids.device)
@@ -283,13 +286,20 @@ def decode_advance(next_ids: torch.Tensor, ids: torch.Tensor, positions: torch.T
         _check(argmax_keys, "argmax_keys", torch.int64, device=next_ids.device)
         _need(argmax_keys.dim() == 2 and argmax_keys.shape[0] == rows, "argmax_keys must be [rows, n]")
         num_keys = argmax_keys.shape[1]
+    _need((embed_table is None) == (embed_out is None), "embed_table and embed_out go together")
+    vocab = hidden = 0
+    if embed_table is not None:
+        _check(embed_table, "embed_table", BF16, device=next_ids.device)
+        _need(embed_table.dim() == 2, "embed_table must be [vocab, hidden]")
+        vocab, hidden = embed_table.shape
+        _check(embed_out, "embed_out", BF16, rows * hidden, next_ids.device)
     call("smx_decode_advance", _stream(ids), next_ids.data_ptr(),
          argmax_keys.data_ptr() if argmax_keys is not None else None, num_keys,
          forced_ids.data_ptr() if forced_ids is not None else None,
          forced_len.data_ptr() if forced_len is not None else None, ids.data_ptr(),
          positions.data_ptr(), seq_lens.data_ptr(), slot_mapping.data_ptr(), block_table.data_ptr(),
          tokens_out.data_ptr() if tokens_out is not None else None, rows, block_table.shape[1],
-         block_size, max_len)
+         block_size, max_len, _ptr(embed_table), _ptr(embed_out), vocab, hidden)
 
 
 def _norm_gemv_checks(x, residual, gamma, residual_out, k):

@@ -62,10 +62,12 @@ def test_bindings_cover_header():
     ("smx_silu_mul", (None, 16, 16, 0, 10)),
     ("smx_embedding", (None, 16, 16, 16, 0, 10, 10)),
     ("smx_argmax_bf16", (None, 16, 0, 10, 16)),
-    ("smx_decode_advance", (None, 16, None, 0, None, None, 16, 16, 16, 16, 16, None, 0, 1, 1, 0)),
-    ("smx_decode_advance", (None, 16, None, 0, None, 16, 16, 16, 16, 16, 16, None, 1, 1, 1, 0)),
-    ("smx_decode_advance", (None, 16, None, 0, 16, 16, 16, 16, 16, 16, 16, None, 1, 1, 1, 0)),
-    ("smx_decode_advance", (None, 16, 16, 0, None, None, 16, 16, 16, 16, 16, None, 1, 1, 1, 0)),
+    ("smx_decode_advance", (None, 16, None, 0, None, None, 16, 16, 16, 16, 16, None, 0, 1, 1, 0, None, None, 0, 0)),
+    ("smx_decode_advance", (None, 16, None, 0, None, 16, 16, 16, 16, 16, 16, None, 1, 1, 1, 0, None, None, 0, 0)),
+    ("smx_decode_advance", (None, 16, None, 0, 16, 16, 16, 16, 16, 16, 16, None, 1, 1, 1, 0, None, None, 0, 0)),
+    ("smx_decode_advance", (None, 16, 16, 0, None, None, 16, 16, 16, 16, 16, None, 1, 1, 1, 0, None, None, 0, 0)),
+    ("smx_decode_advance", (None, 16, None, 0, None, None, 16, 16, 16, 16, 16, None, 1, 1, 1, 0, 16, None, 8, 8)),
+    ("smx_decode_advance", (None, 16, None, 0, None, None, 16, 16, 16, 16, 16, None, 1, 1, 1, 0, 16, 16, 0, 8)),
     ("smx_q4_0_add_rmsnorm_gemv", (None, 16, 16, 16, 16, 16, 16, 64, 96, 1e-6)),
     ("smx_q4_0_add_rmsnorm_gemv", (None, 16, 16, 16, 16, 16, 16, 64, 256, 1e-6)),
     ("smx_q4_0_add_rmsnorm_gemv", (None, 16, 32, 16, 32, 16, 16, 64, 256, 1e-6)),

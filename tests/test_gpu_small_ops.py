@@ -135,3 +135,40 @@ def test_decode_advance(ops, dev):
     pos.fill_(3 * 128 - 1)
     ops.decode_advance(nxt, ids, pos, sl, slots, table, 128)
     assert slots.tolist() == [-1, -1]
+
+
+def test_decode_advance_gathers_next_embedding(ops, dev):
+    """With an embedding table, the advance kernel leaves the embedding row of
+    each row's new id (the argmax of its keys, or the forced token), zeros
+    for an id outside the vocab; the ids and positions are as without it."""
+    import torch
+    rng = np.random.default_rng(3)
+    vocab, hidden, rows = 50, 2560, 3
+    table = randn_bf16(rng, (vocab, hidden))
+    tdev = bf16_dev(table, dev).view(vocab, hidden)
+    keys = torch.zeros((rows, 700), dtype=torch.int64, device=dev)
+    # row r's best key sits at index 500 + r with id 7 * r; ids are encoded
+    # as 0xffffffff - id in the low word under a positive value key
+    for r in range(rows):
+        keys[r, 500 + r] = (0x9000 << 32) | (0xFFFFFFFF - 7 * r)
+    nxt = torch.zeros(rows, dtype=torch.int64, device=dev)
+    ids = torch.zeros(rows, dtype=torch.int64, device=dev)
+    pos = torch.tensor([3, 9, 0], dtype=torch.int64, device=dev)
+    sl = pos.to(torch.int32) + 1
+    slots = torch.zeros(rows, dtype=torch.int64, device=dev)
+    table_bt = torch.arange(rows * 4, dtype=torch.int32, device=dev).view(rows, 4)
+    forced = torch.full((rows, 16), -1, dtype=torch.int64, device=dev)
+    forced[1, 10] = 49          # row 1 takes a forced token
+    forced[2, 1] = vocab + 5    # row 2 a forced id outside the vocab
+    flen = torch.tensor([0, 11, 2], dtype=torch.int32, device=dev)
+    out = torch.full((rows, hidden), 7.0, dtype=torch.bfloat16, device=dev)
+    ops.decode_advance(nxt, ids, pos, sl, slots, table_bt, 128, forced_ids=forced,
+                       forced_len=flen, argmax_keys=keys.view(rows, -1), embed_table=tdev,
+                       embed_out=out)
+    assert nxt.tolist() == [0, 7, 14]
+    assert ids.tolist() == [0, 49, vocab + 5]
+    assert pos.tolist() == [4, 10, 1]
+    got = bits_of(out).reshape(rows, hidden)
+    np.testing.assert_array_equal(got[0], table[0])
+    np.testing.assert_array_equal(got[1], table[49])
+    assert np.all(got[2] == 0)
