@@ -158,6 +158,14 @@ __global__ __launch_bounds__(512) void q4_0_gemm_kernel(GemmArgs a) {
 
 #include "smx_abi_util.h"
 
+namespace smx {
+// Multi-row streaming GEMV (q4_0_gemv.hip); hipErrorNotSupported for shapes
+// it does not take (then the MFMA kernel above runs).
+hipError_t q4_0_gemv_rows(hipStream_t s, const void* x, const void* w, void* y, int64_t m,
+                          int64_t n_out, int64_t k, int64_t ldx, int64_t ldy, bool swiglu,
+                          int64_t up_offset_rows);
+}  // namespace smx
+
 #define SMX_GEMM_CHECKS(N)                                                                      \
   SMX_REQUIRE(x && w && y, "null pointer argument");                                            \
   SMX_REQUIRE(m >= 1 && m <= 16, "m must be in [1, 16]");                                       \
@@ -169,6 +177,10 @@ __global__ __launch_bounds__(512) void q4_0_gemm_kernel(GemmArgs a) {
 extern "C" int smx_q4_0_gemm(void* stream, const void* x, const void* w, void* y, int64_t m,
                              int64_t n, int64_t k) {
   SMX_GEMM_CHECKS(n);
+  {
+    const hipError_t e = smx::q4_0_gemv_rows((hipStream_t)stream, x, w, y, m, n, k, k, n, false, 0);
+    if (e != hipErrorNotSupported) return (int)e;
+  }
   smx::GemmArgs a{(const uint16_t*)x, (const uint8_t*)w, (uint16_t*)y, (int)m, (int)n,
                   (int)(k / 64), k, n, 0};
   hipLaunchKernelGGL(smx::q4_0_gemm_kernel<false>, dim3((unsigned)((n + 15) / 16)), dim3(512), 0,
@@ -179,6 +191,10 @@ extern "C" int smx_q4_0_gemm(void* stream, const void* x, const void* w, void* y
 extern "C" int smx_q4_0_gemm_swiglu(void* stream, const void* x, const void* w, void* y,
                                     int64_t m, int64_t d, int64_t k) {
   SMX_GEMM_CHECKS(d);
+  {
+    const hipError_t e = smx::q4_0_gemv_rows((hipStream_t)stream, x, w, y, m, d, k, k, d, true, d);
+    if (e != hipErrorNotSupported) return (int)e;
+  }
   smx::GemmArgs a{(const uint16_t*)x, (const uint8_t*)w, (uint16_t*)y, (int)m, (int)d,
                   (int)(k / 64), k, d, d};
   hipLaunchKernelGGL(smx::q4_0_gemm_kernel<true>, dim3((unsigned)((d + 7) / 8)), dim3(512), 0,

@@ -1,4 +1,5 @@
-"""GPU parity of the batched Q4_0 GEMM (MFMA) through the C ABI: each output
+"""GPU parity of the batched Q4_0 GEMM (streaming multi-row kernel for up to
+8 rows, MFMA above) through the C ABI: each output
 row within 1e-2 relative of the float64 oracle GEMV of that activation row;
 one-hot activations select dequantised weights bit-exactly (this pins the
 MFMA operand and result layouts); SwiGLU epilogue; writes stay in bounds."""
@@ -44,13 +45,15 @@ def test_gemm_vs_oracle(ops, dev, m, n, k):
                          what=f"row {r}")
 
 
-def test_gemm_one_hot_layout(ops, dev):
+@pytest.mark.parametrize("m", [3, 8, 16])
+def test_gemm_one_hot_layout(ops, dev, m):
     """Row m of x is one-hot at column c_m: y[m][n] = bf16(dequant(W)[n][c_m])
-    exactly, for 16 rows, 48 output rows and columns spread over both blocks
-    of a pair and all nibble positions."""
-    n, k, m = 48, 256, 16
+    exactly, for up to 16 rows (m <= 8: the streaming multi-row kernel, else
+    the MFMA kernel), 48 output rows and columns spread over both blocks of a
+    pair and all nibble positions."""
+    n, k = 48, 256
     blocks = oq.make_blocks(n, k, seed=11, scale=1.0)
-    cols = np.array([0, 1, 14, 15, 16, 17, 30, 31, 32, 33, 46, 47, 48, 63, 100, 255])
+    cols = np.array([0, 1, 14, 15, 16, 17, 30, 31, 32, 33, 46, 47, 48, 63, 100, 255])[:m]
     x = np.zeros((m, k), dtype=np.uint16)
     x[np.arange(m), cols] = f32_to_bf16_bits(np.float32([1.0]))[0]
     y = bits_of(ops.q4_0_gemm(bf16_dev(x, dev), _w(blocks, dev), n, k)).reshape(m, n)
