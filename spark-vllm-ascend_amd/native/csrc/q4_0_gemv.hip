@@ -190,9 +190,17 @@ __global__ __launch_bounds__(NPMAX <= 2 ? 1024 : 512) void q4_0_gemv_kernel(
     }
   }
 
-  // 2. Every weight load of this wave (rows past n_out and pairs past the
+  // 2. The weight loads of this wave (rows past n_out and pairs past the
   //    row end read the last valid row / pair; their results are dropped).
+  //    PRO with several row groups issues only the first half here and the
+  //    rest after the prologue: a wave stalls at issue while the CU's memory
+  //    pipeline is full of other waves' weight requests, and the prologue's
+  //    barrier waits for the slowest wave, so fewer loads ahead of it end the
+  //    prologue earlier while half the weights are already in flight
+  //    (measured: all loads ahead, half, or none -- half is fastest; with a
+  //    single row group all ahead is).
   constexpr int OUT_PER_GROUP = SWIGLU ? 4 : 8;
+  constexpr int GEARLY = PRO && RG > 1 ? RG / 2 : RG;
   int64_t wrow[RG];
 #pragma unroll
   for (int g = 0; g < RG; ++g) {
@@ -201,14 +209,17 @@ __global__ __launch_bounds__(NPMAX <= 2 ? 1024 : 512) void q4_0_gemv_kernel(
     wrow[g] = SWIGLU ? (oc + ((rsub >> 2) ? a.up_offset_rows : 0)) : oc;
   }
   Pair wp[RG][NPMAX];
+  auto load_groups = [&](int g0, int g1) {
 #pragma unroll
-  for (int g = 0; g < RG; ++g) {
+    for (int g = g0; g < g1; ++g) {
 #pragma unroll
-    for (int t = 0; t < NPMAX; ++t) {
-      const int j = min((wave + ks * t) * 8 + col, npairs - 1);
-      wp[g][t] = load_pair(a.w + wrow[g] * row_bytes + 36 * j);
+      for (int t = 0; t < NPMAX; ++t) {
+        const int j = min((wave + ks * t) * 8 + col, npairs - 1);
+        wp[g][t] = load_pair(a.w + wrow[g] * row_bytes + 36 * j);
+      }
     }
-  }
+  };
+  load_groups(0, GEARLY);
 #pragma unroll
   for (int t = 0; t < NPMAX; ++t) {
     if (!xok[t]) xv[t] = u32x4{0u, 0u, 0u, 0u};
@@ -274,6 +285,7 @@ __global__ __launch_bounds__(NPMAX <= 2 ? 1024 : 512) void q4_0_gemv_kernel(
     *reinterpret_cast<u32x4*>(rec + 4 * (lane & 7)) = v;
     if ((lane & 3) == 0) rec[32 + ((lane >> 2) & 1)] = __float_as_uint(-136.0f * s);
   }
+  load_groups(GEARLY, RG);  // the rest of the weights (PRO with RG > 1)
   // The slice is private to this wave: LDS operations of one wave complete
   // in order, so only the compiler has to be kept from reordering.
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");

@@ -75,8 +75,39 @@ __device__ __forceinline__ float sum4(float v) {
   return v;
 }
 
-__device__ __forceinline__ float shfl_xor_f32(float v, int mask) {
-  return __shfl_xor(v, mask, 64);
+// This lane's value and that of lane ^ MASK (MASK 16 or 32), in an order that
+// differs between the two lanes: v_permlane16_swap_b32 / v_permlane32_swap_b32
+// of a register with itself exchange its odd 16-lane rows (odd 32-lane
+// halves) with the even ones of the copy, so each lane ends with {own,
+// partner}.  Plain VALU operations, where __shfl_xor goes through the LDS
+// crossbar (ds_bpermute, an LDS round trip).  All 64 lanes must be active.
+// Sums and maxima over the pair are commutative, so every lane of a pair
+// gets the same bits.
+template <int MASK>
+__device__ __forceinline__ void lane_pair(float v, float& a, float& b) {
+  static_assert(MASK == 16 || MASK == 32, "row swaps of 16 or 32 lanes");
+  const uint32_t u = __float_as_uint(v);
+  if constexpr (MASK == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    a = __uint_as_float(r[0]);
+    b = __uint_as_float(r[1]);
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    a = __uint_as_float(r[0]);
+    b = __uint_as_float(r[1]);
+  }
+}
+template <int MASK>
+__device__ __forceinline__ float xor_sum(float v) {
+  float a, b;
+  lane_pair<MASK>(v, a, b);
+  return a + b;
+}
+template <int MASK>
+__device__ __forceinline__ float xor_max(float v) {
+  float a, b;
+  lane_pair<MASK>(v, a, b);
+  return fmaxf(a, b);
 }
 
 // Full-wave reductions.
@@ -85,8 +116,8 @@ __device__ __forceinline__ float wave_sum(float v) {
   v += dpp_f32<DPP_QUAD_XOR2>(v);
   v += dpp_f32<DPP_ROW_HALF_MIRROR>(v);
   v += dpp_f32<DPP_ROW_MIRROR>(v);
-  v += shfl_xor_f32(v, 16);
-  v += shfl_xor_f32(v, 32);
+  v = xor_sum<16>(v);
+  v = xor_sum<32>(v);
   return v;
 }
 

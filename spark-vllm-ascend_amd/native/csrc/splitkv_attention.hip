@@ -35,8 +35,8 @@ constexpr int DPP_ROW_ROR8 = 0x128;
 __device__ __forceinline__ float sum_stride4(float v) {
   v += dppf<DPP_ROW_ROR4>(v);
   v += dppf<DPP_ROW_ROR8>(v);
-  v += shfl_xor_f32(v, 16);
-  v += shfl_xor_f32(v, 32);
+  v = xor_sum<16>(v);
+  v = xor_sum<32>(v);
   return v;
 }
 
@@ -44,8 +44,8 @@ __device__ __forceinline__ float sum_stride4(float v) {
 __device__ __forceinline__ float max_stride4(float v) {
   v = fmaxf(v, dppf<DPP_ROW_ROR4>(v));
   v = fmaxf(v, dppf<DPP_ROW_ROR8>(v));
-  v = fmaxf(v, shfl_xor_f32(v, 16));
-  v = fmaxf(v, shfl_xor_f32(v, 32));
+  v = xor_max<16>(v);
+  v = xor_max<32>(v);
   return v;
 }
 
@@ -442,10 +442,7 @@ __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(
   for (int h = 0; h < G; ++h)
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      float v = o[h][i];
-      v += shfl_xor_f32(v, 16);
-      v += shfl_xor_f32(v, 32);
-      o[h][i] = v;
+      o[h][i] = xor_sum<32>(xor_sum<16>(o[h][i]));
     }
   if (vt == 0) {
 #pragma unroll
@@ -490,8 +487,8 @@ __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp_f32<DPP_QUAD_XOR2>(v));
   v = fmaxf(v, dpp_f32<DPP_ROW_HALF_MIRROR>(v));
   v = fmaxf(v, dpp_f32<DPP_ROW_MIRROR>(v));
-  v = fmaxf(v, shfl_xor_f32(v, 16));
-  v = fmaxf(v, shfl_xor_f32(v, 32));
+  v = xor_max<16>(v);
+  v = xor_max<32>(v);
   return v;
 }
 
