@@ -26,28 +26,7 @@ constexpr int HD = 128;
 constexpr int G = 4;       // q heads per kv head
 constexpr int TILE = 32;   // tokens per wave iteration
 
-template <int CTRL>
-__device__ __forceinline__ float dppf(float v) { return dpp_f32<CTRL>(v); }
-constexpr int DPP_ROW_ROR4 = 0x124;
-constexpr int DPP_ROW_ROR8 = 0x128;
-
-// sum over the 16 lanes of a wave that share lane & 3
-__device__ __forceinline__ float sum_stride4(float v) {
-  v += dppf<DPP_ROW_ROR4>(v);
-  v += dppf<DPP_ROW_ROR8>(v);
-  v = xor_sum<16>(v);
-  v = xor_sum<32>(v);
-  return v;
-}
-
-// Max over the 16 lanes of a wave that share lane & 3.
-__device__ __forceinline__ float max_stride4(float v) {
-  v = fmaxf(v, dppf<DPP_ROW_ROR4>(v));
-  v = fmaxf(v, dppf<DPP_ROW_ROR8>(v));
-  v = xor_max<16>(v);
-  v = xor_max<32>(v);
-  return v;
-}
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 
 // One workgroup of WAVES waves per (split, kv head, sequence).  Split s
@@ -126,7 +105,6 @@ __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(
   A.n_kv = n_kv_;
   A.n_q = 4 * n_kv_;  // GQA 4:1 (validated on the host)
   static_assert(BLK == 32 || BLK == 64, "blocks of 32 or 64 tokens");
-  constexpr int RB = BLK / 8;  // 8-token steps per block
   const uint16_t* __restrict__ kc = A.kc;
   const uint16_t* __restrict__ vc = A.vc;
   const int32_t* __restrict__ block_table = A.block_table;
@@ -137,8 +115,8 @@ __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(
   const float scale_log2 = A.scale_log2;
   constexpr int NT = 64 * WAVES;
   __shared__ __attribute__((aligned(16))) uint32_t q_lds[G * HD / 2];  // 4 heads, bf16 pairs
-  __shared__ __attribute__((aligned(16))) uint32_t p2[WAVES][2 * BLK];  // [jp RB][vt 4][h 4]
-  __shared__ float o_w[WAVES][G * HD];
+  __shared__ __attribute__((aligned(16))) uint32_t p2[WAVES][2 * BLK];  // P: bf16 [head][token]
+  __shared__ __attribute__((aligned(16))) float o_w[WAVES][G * HD];
   __shared__ float m_w[WAVES][G], l_w[WAVES][G];
   __shared__ int bad_w[WAVES];
 
@@ -227,9 +205,10 @@ __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(
   const int64_t tok_stride = (int64_t)n_kv * HD;
   const int64_t page_stride = tok_stride << bs_log2;
 
-  const int tok = lane >> 3, dq = lane & 7;  // QK: token slot, 16-byte chunks dq, dq + 8
-  const int hsel = lane & 3;                 // softmax: the head this lane keeps
-  const int vt = lane >> 4, dv = lane & 15;  // PV: token slot, 8-dim slice
+  // Lane roles of v_mfma_f32_16x16x32_bf16: lane l = 16 g + n holds row n of
+  // A and column n of B at k = 8 g .. 8 g + 7, and rows 4 g .. 4 g + 3 of
+  // column n of C.
+  const int n = lane & 15, g = lane >> 4;
 
   // A block-table entry outside [0, num_blocks) is never dereferenced: the
   // page is replaced by page 0 and the partial is poisoned with NaN below.
@@ -247,10 +226,16 @@ __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(
     if (!has_work) pg = t = 0;
     return (int64_t)pg * page_stride + (int64_t)(t & (bs - 1)) * tok_stride + kvh * HD;
   };
-  // Every K and V load of one 64-token block; tokens past the chunk end are
-  // loaded from the block's first token (always valid) instead of branching,
-  // and their scores are masked to -inf.
-  u32x4 kr[RB][2], vr[RB][2];
+  // Every K and V load of one block, in the MFMA operand layouts; tokens past
+  // the chunk end are loaded from the block's first token (always valid)
+  // instead of branching, and their scores are masked to -inf.
+  //  K (QK A operand, per 16-token tile tt and 32-dim step ks): token
+  //    16 tt + n, dims 32 ks + 8 g .. + 8 -- 16 tokens x 64 bytes per load.
+  //  V (per 32-token step sb, transposed in registers into the PV B
+  //    operands): tokens 32 sb + 8 g + j (j < 8), dims 8 n .. 8 n + 7 -- four
+  //    whole 256-byte rows per load.
+  constexpr int NT16 = BLK / 16, NS32 = BLK / 32;
+  u32x4 kr[NT16][4], vr[NS32][8];
   auto load_block = [&](int t0) {
     const int64_t b0 = half_base(t0, t0 == w0 ? bt0 : bt[t0 >> bs_log2]);
     const int64_t b1 = BLK == 64 && t0 + 32 < w1
@@ -261,16 +246,16 @@ __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(
       return (te < 32 ? b0 : b1) + (int64_t)(te & 31) * tok_stride;
     };
 #pragma unroll
-    for (int r = 0; r < RB; ++r) {
-      const uint16_t* p = kc + tok_off(8 * r + tok);
-      kr[r][0] = reinterpret_cast<const u32x4*>(p)[dq];
-      kr[r][1] = reinterpret_cast<const u32x4*>(p)[dq + 8];
+    for (int tt = 0; tt < NT16; ++tt) {
+      const u32x4* kp = reinterpret_cast<const u32x4*>(kc + tok_off(16 * tt + n));
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) kr[tt][ks] = kp[4 * ks + g];
     }
 #pragma unroll
-    for (int jp = 0; jp < RB; ++jp)
+    for (int sb = 0; sb < NS32; ++sb)
 #pragma unroll
-      for (int hf = 0; hf < 2; ++hf)
-        vr[jp][hf] = reinterpret_cast<const u32x4*>(vc + tok_off(8 * jp + vt + 4 * hf))[dv];
+      for (int j = 0; j < 8; ++j)
+        vr[sb][j] = reinterpret_cast<const u32x4*>(vc + tok_off(32 * sb + 8 * g + j))[n];
   };
   // The rotary row (its address needs the position) and the first K/V block
   // (its pages) follow in the second round trip; the q/k norm + RoPE + KV
@@ -322,20 +307,23 @@ __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(
   }
 
   __syncthreads();
-  u32x4 qr[G][2];
+  // q as the QK B operand: column n = head n < G at the lane's dims (columns
+  // n >= G are zero; their scores are computed and never used).
+  u32x4 qop[4];
 #pragma unroll
-  for (int h = 0; h < G; ++h) {
-    qr[h][0] = reinterpret_cast<const u32x4*>(q_lds)[h * 16 + dq];
-    qr[h][1] = reinterpret_cast<const u32x4*>(q_lds)[h * 16 + dq + 8];
+  for (int ks = 0; ks < 4; ++ks) {
+    const u32x4 v = reinterpret_cast<const u32x4*>(q_lds)[(n & (G - 1)) * 16 + 4 * ks + g];
+    qop[ks] = n < G ? v : u32x4{0u, 0u, 0u, 0u};
   }
 
-  float m_mine = -INFINITY;  // running max (log2 domain) of head hsel
-  float l_lane = 0.f;        // running sum of head hsel over this lane's tokens
-  float o[G][8];
+  float m_mine = -INFINITY;  // running max (log2 domain) of head n (lanes n < G)
+  float l_lane = 0.f;        // running sum of head n over this lane's tokens
+  // PV accumulators, one C tile per dim group T: lane l < 16 holds heads
+  // 0..3 of dim 8 l + T (rows 4..15 of every tile are the zero heads).
+  f32x4 acc[8];
 #pragma unroll
-  for (int h = 0; h < G; ++h)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) o[h][i] = 0.f;
+  for (int t = 0; t < 8; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  uint16_t* pw = reinterpret_cast<uint16_t*>(p2[wave]);  // P as bf16 [head G][BLK]
 
   for (int t0 = w0; t0 < w1; t0 += BLK) {
     if (t0 != w0) load_block(t0);
@@ -345,91 +333,91 @@ __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(
       // same launch, which does not order the store before these loads).
       const int tp = (int)(pos - t0);
       if (owner && tp >= 0 && tp < BLK) {
+        const u32x4* kn = reinterpret_cast<const u32x4*>(kv_new[0]);
+        const u32x4* vn = reinterpret_cast<const u32x4*>(kv_new[1]);
 #pragma unroll
-        for (int r = 0; r < RB; ++r)
-          if (8 * r + tok == tp) {
-            kr[r][0] = reinterpret_cast<const u32x4*>(kv_new[0])[dq];
-            kr[r][1] = reinterpret_cast<const u32x4*>(kv_new[0])[dq + 8];
+        for (int tt = 0; tt < NT16; ++tt)
+          if (16 * tt + n == tp) {
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) kr[tt][ks] = kn[4 * ks + g];
           }
 #pragma unroll
-        for (int jp = 0; jp < RB; ++jp)
+        for (int sb = 0; sb < NS32; ++sb)
 #pragma unroll
-          for (int hf = 0; hf < 2; ++hf)
-            if (8 * jp + vt + 4 * hf == tp) vr[jp][hf] = reinterpret_cast<const u32x4*>(kv_new[1])[dv];
+          for (int j = 0; j < 8; ++j)
+            if (32 * sb + 8 * g + j == tp) vr[sb][j] = vn[n];
       }
     }
-    // ---- scores: token 8r + tok, head hsel
-    float sm[RB];
+    // ---- scores S[token][head]: lane (n, g) gets tokens 16 tt + 4 g + i of head n
+    float sc[NT16][4];
 #pragma unroll
-    for (int r = 0; r < RB; ++r) {
-      float a[G];
+    for (int tt = 0; tt < NT16; ++tt) {
+      f32x4 c = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int h = 0; h < G; ++h) {
-        float x = 0.f;
+      for (int ks = 0; ks < 4; ++ks)
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[tt][ks]),
+                                                    __builtin_bit_cast(bf16x8, qop[ks]), c, 0, 0,
+                                                    0);
 #pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          x = dot2_bf16(qr[h][c].x, kr[r][c].x, x);
-          x = dot2_bf16(qr[h][c].y, kr[r][c].y, x);
-          x = dot2_bf16(qr[h][c].z, kr[r][c].z, x);
-          x = dot2_bf16(qr[h][c].w, kr[r][c].w, x);
-        }
-        a[h] = sum8(x);
-      }
-      const float sv = hsel == 0 ? a[0] : hsel == 1 ? a[1] : hsel == 2 ? a[2] : a[3];
-      sm[r] = (t0 + 8 * r + tok < w1) ? sv * scale_log2 : -INFINITY;
+      for (int i = 0; i < 4; ++i)
+        sc[tt][i] = (t0 + 16 * tt + 4 * g + i < w1) ? c[i] * scale_log2 : -INFINITY;
     }
-    // ---- online softmax (log2 domain) for head hsel
-    float mx = sm[0];
+    // ---- online softmax (log2 domain) of head n over the lanes n + 16 g
+    float mx = sc[0][0];
 #pragma unroll
-    for (int r = 1; r < RB; ++r) mx = fmaxf(mx, sm[r]);
-    mx = max_stride4(mx);
+    for (int tt = 0; tt < NT16; ++tt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[tt][i]);
+    mx = xor_max<32>(xor_max<16>(mx));
     const float mn = fmaxf(m_mine, mx);
     const float alpha = exp2f(m_mine - mn);
     m_mine = mn;
-    const bool writer = (lane & 4) == 0;  // lanes dq and dq + 4 hold the same head
     float psum = 0.f;
 #pragma unroll
-    for (int r = 0; r < RB; ++r) {
-      const float p = exp2f(sm[r] - mn);
-      psum += p;
-      if (writer) {
-        uint16_t* dst = reinterpret_cast<uint16_t*>(&p2[wave][(r * 4 + (tok & 3)) * 4 + hsel]);
-        dst[tok >> 2] = f32_to_bf16(p);
-      }
-    }
-    l_lane = l_lane * alpha + (writer ? psum : 0.f);
-    float alpha_h[G];
+    for (int tt = 0; tt < NT16; ++tt) {
+      float pv[4];
 #pragma unroll
-    for (int h = 0; h < G; ++h)
-      alpha_h[h] = __builtin_bit_cast(float,
-                                      __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), h));
+      for (int i = 0; i < 4; ++i) {
+        pv[i] = exp2f(sc[tt][i] - mn);
+        psum += pv[i];
+      }
+      if (n < G)
+        *reinterpret_cast<u32x2*>(pw + n * BLK + 16 * tt + 4 * g) =
+            u32x2{pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3])};
+    }
+    l_lane = l_lane * alpha + psum;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-    // ---- O = O * alpha + P V
-#pragma unroll
-    for (int h = 0; h < G; ++h)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) o[h][i] *= alpha_h[h];
-#pragma unroll
-    for (int jp = 0; jp < RB; ++jp) {
-      const u32x4 pp = *reinterpret_cast<const u32x4*>(&p2[wave][(jp * 4 + vt) * 4]);
-      const u32x4 va = vr[jp][0], vb2 = vr[jp][1];
-      uint32_t vpair[8];  // (v[t1][d], v[t2][d]) for the 8 dims
-      vpair[0] = perm_b32(vb2.x, va.x, 0x05040100u);
-      vpair[1] = perm_b32(vb2.x, va.x, 0x07060302u);
-      vpair[2] = perm_b32(vb2.y, va.y, 0x05040100u);
-      vpair[3] = perm_b32(vb2.y, va.y, 0x07060302u);
-      vpair[4] = perm_b32(vb2.z, va.z, 0x05040100u);
-      vpair[5] = perm_b32(vb2.z, va.z, 0x07060302u);
-      vpair[6] = perm_b32(vb2.w, va.w, 0x05040100u);
-      vpair[7] = perm_b32(vb2.w, va.w, 0x07060302u);
-      const uint32_t ph[G] = {pp.x, pp.y, pp.z, pp.w};
+    // ---- O = O * alpha + P V (the first block starts from O = 0)
+    if (t0 != w0) {
+      float alpha_h[G];
 #pragma unroll
       for (int h = 0; h < G; ++h)
+        alpha_h[h] = __builtin_bit_cast(
+            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), h));
 #pragma unroll
-        for (int i = 0; i < 8; ++i) o[h][i] = dot2_bf16(ph[h], vpair[i], o[h][i]);
+      for (int t = 0; t < 8; ++t)
+#pragma unroll
+        for (int r = 0; r < G; ++r) acc[t][r] *= alpha_h[r];
+    }
+#pragma unroll
+    for (int sb = 0; sb < NS32; ++sb) {
+      // A = P: row n = head n < G, tokens 32 sb + 8 g .. + 8
+      const u32x4 pr = *reinterpret_cast<const u32x4*>(pw + (n & (G - 1)) * BLK + 32 * sb + 8 * g);
+      const u32x4 pa = n < G ? pr : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        // B = V^T for dim group t: element 2i / 2i + 1 = tokens 8 g + 2i / + 1 at dim 8 n + t
+        const uint32_t sel = (t & 1) ? 0x07060302u : 0x05040100u;
+        uint32_t bw[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) bw[i] = perm_b32(vr[sb][2 * i + 1][t >> 1], vr[sb][2 * i][t >> 1], sel);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, pa),
+                                                         __builtin_bit_cast(bf16x8, bw), acc[t],
+                                                         0, 0, 0);
+      }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -437,18 +425,14 @@ __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(
   }
 
   // ---- per-wave state to LDS
-  const float l_tot = sum_stride4(l_lane);
+  const float l_tot = xor_sum<32>(xor_sum<16>(l_lane));
+  if (lane < 16) {
 #pragma unroll
-  for (int h = 0; h < G; ++h)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      o[h][i] = xor_sum<32>(xor_sum<16>(o[h][i]));
+    for (int r = 0; r < G; ++r) {
+      float* dst = &o_w[wave][r * HD + 8 * lane];
+      *reinterpret_cast<f32x4*>(dst) = f32x4{acc[0][r], acc[1][r], acc[2][r], acc[3][r]};
+      *reinterpret_cast<f32x4*>(dst + 4) = f32x4{acc[4][r], acc[5][r], acc[6][r], acc[7][r]};
     }
-  if (vt == 0) {
-#pragma unroll
-    for (int h = 0; h < G; ++h)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) o_w[wave][h * HD + 8 * dv + i] = o[h][i];
   }
   if (lane == 0) bad_w[wave] = bad_page ? 1 : 0;
   if (lane < G) {
