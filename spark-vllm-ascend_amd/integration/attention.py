@@ -41,9 +41,11 @@ def choose_num_splits(capacity: int, tokens_per_split: int = 128) -> int:
     """Split count for a block table addressing `capacity` tokens.  Splits
     are cut from the capacity (not the current length), so one captured graph
     serves every step.  Measured on MI355X: 128 tokens per split (four waves
-    of one 32-token block each) is best for several sequences at long
-    contexts (8 sequences at 6k..31k); one sequence at 2k..6k decodes 1.3%
-    faster with 192 (six waves), fewer workgroups and a smaller merge."""
+    of one 32-token block each, two workgroups per CU) is best for one
+    sequence at 2k..6k (49 splits at a 6272-token capacity; 32 or 33 splits
+    of 224 / 192 tokens put one 8-wave workgroup on a CU, and past 256
+    workgroups the rest run in a second round) and for 8 sequences at
+    6k..31k."""
     return int(max(1, -(-capacity // tokens_per_split)))
 
 

@@ -197,10 +197,11 @@ __global__ __launch_bounds__(NPMAX <= 2 ? 1024 : 512) void q4_0_gemv_kernel(
   //    pipeline is full of other waves' weight requests, and the prologue's
   //    barrier waits for the slowest wave, so fewer loads ahead of it end the
   //    prologue earlier while half the weights are already in flight
-  //    (measured: all loads ahead, half, or none -- half is fastest; with a
-  //    single row group all ahead is).
+  //    (measured in the decode step: for norm + gate/up all loads ahead,
+  //    half, or none -- half is fastest; with a single row group, and for
+  //    the 9496-workgroup head, all ahead is).
   constexpr int OUT_PER_GROUP = SWIGLU ? 4 : 8;
-  constexpr int GEARLY = PRO && RG > 1 ? RG / 2 : RG;
+  constexpr int GEARLY = PRO && RG > 1 && EPI != EPI_ARGMAX ? RG / 2 : RG;
   int64_t wrow[RG];
 #pragma unroll
   for (int g = 0; g < RG; ++g) {
@@ -614,19 +615,31 @@ struct GemvShape {
   int rg, ks, np;
 };
 
-static GemvShape pick_shape(int n_out, int out_per_group, int ngroups, bool norm_swiglu) {
-  // Measured on MI355X (graph-replayed launches over rotating weights):
+// What the GEMV fuses, as far as the launch shape goes.
+enum { KIND_PLAIN = 0, KIND_NORM_STORE = 1, KIND_NORM_SWIGLU = 2 };
+
+static GemvShape pick_shape(int n_out, int out_per_group, int ngroups, int kind) {
+  // Measured on MI355X, in the decode step and on graph-replayed launches
+  // over rotating weights:
   //  * every pair group of a row gets its own wave (np = 1) up to 16 waves
-  //    per workgroup -- shorter per-wave work beats fewer, longer waves;
-  //  * 16 rows per workgroup (rg = 2) for long rows (K >= 4096), for very
-  //    tall matrices (the 151936-row head) and for the norm + SwiGLU
-  //    variant; 8 rows otherwise (6144/9728 x 2560).
+  //    per workgroup -- shorter per-wave work beats fewer, longer waves --
+  //    and 17..32 pair groups take 16 waves with two groups on the first
+  //    ones (2560 x 9728: 16 waves beat 10 balanced ones);
+  //  * the norm-fused plain GEMV (QKV 6144 x 2560) takes two pair groups
+  //    per wave: fewer waves meet at the prologue's barrier;
+  //  * 16 rows per workgroup (rg = 2) above 8 pair groups (K > 4096), for
+  //    very tall matrices (the 151936-row head) and for the norm + SwiGLU
+  //    variant; 8 rows otherwise (6144/9728 x 2560, 2560 x 4096).
   GemvShape sh;
   const int wgs1 = (n_out + out_per_group - 1) / out_per_group;
-  sh.rg = (ngroups >= 8 || wgs1 >= 8192 || norm_swiglu) ? 2 : 1;
-  sh.np = (ngroups + 15) / 16;
-  sh.ks = (ngroups + sh.np - 1) / sh.np;
-  if (sh.np > 2) {  // above 2 pair groups per lane, at most 8 waves per workgroup
+  sh.rg = (ngroups > 8 || wgs1 >= 8192 || kind == KIND_NORM_SWIGLU) ? 2 : 1;
+  if (ngroups <= 16) {
+    sh.np = kind == KIND_NORM_STORE && ngroups > 2 ? 2 : 1;
+    sh.ks = (ngroups + sh.np - 1) / sh.np;
+  } else if (ngroups <= 32) {
+    sh.np = 2;
+    sh.ks = 16;
+  } else {  // above 2 pair groups per lane, at most 8 waves per workgroup
     sh.np = (ngroups + 7) / 8;
     sh.ks = (ngroups + sh.np - 1) / sh.np;
   }
@@ -678,10 +691,10 @@ static hipError_t dispatch_np(hipStream_t s, const GemvArgs& a, const GemvShape&
 
 // Whether the streaming kernel takes this call (else the generic kernel).
 static bool fast_path(int64_t k, const void* x, const void* w, GemvShape* sh, int64_t n_out,
-                      int out_per_group, bool norm_swiglu = false) {
+                      int out_per_group, int kind = KIND_PLAIN) {
   if (k % 64 != 0 || (uintptr_t)w % 4 != 0 || (uintptr_t)x % 16 != 0) return false;
   const int ngroups = (int)((k / 64 + 7) / 8);
-  *sh = pick_shape((int)n_out, out_per_group, ngroups, norm_swiglu);
+  *sh = pick_shape((int)n_out, out_per_group, ngroups, kind);
   return sh->np <= 8;
 }
 
@@ -696,8 +709,11 @@ static hipError_t gemv_dispatch(hipStream_t s, GemvArgs a, int64_t k, int epi, b
   const int64_t nblocks = k / 32;
   a.npairs = (int)(nblocks / 2);
   GemvShape sh{1, 1, 1};
-  if (!fast_path(k, a.x, a.w, &sh, a.n_out, epi == EPI_SWIGLU ? 4 : 8,
-                 pro && epi == EPI_SWIGLU)) {
+  const int kind = !pro ? KIND_PLAIN
+                   : epi == EPI_SWIGLU ? KIND_NORM_SWIGLU
+                   : epi == EPI_STORE ? KIND_NORM_STORE
+                                      : KIND_PLAIN;
+  if (!fast_path(k, a.x, a.w, &sh, a.n_out, epi == EPI_SWIGLU ? 4 : 8, kind)) {
     if (pro || epi == EPI_ARGMAX) return hipErrorInvalidValue;  // callers check first
     if (epi == EPI_SWIGLU)
       hipLaunchKernelGGL(q4_0_gemv_generic_kernel<true>, dim3((unsigned)a.n_out), dim3(64), 0, s,

@@ -478,35 +478,44 @@ __device__ __forceinline__ float wave_max(float v) {
 
 // Log-sum-exp merge (merge_attention, src/spark_vllm_ascend/kernels/
 // vector.py:61-78): w_s = exp(lse_s - max), out = sum_s w_s o_s / sum_s w_s.
-// One wave per (64 dims of a q head, sequence), splits in chunks of 64:
-// lane j loads the lse of split j (one vector load), the chunk's max and the
-// weight sum are wave reductions and each lane computes one weight; lane d
-// then folds the chunk's partials of its dim with the weights broadcast
-// from their lanes (v_readlane).  Every load of a chunk is unconditional
-// (indices past the last split are clamped, with uniform scalar arithmetic,
-// and carry no weight), so a chunk costs one round trip.  Splits with
-// lse = -inf carry no weight; a NaN lse or partial makes the output NaN; no
-// weight at all gives 0.
-__global__ __launch_bounds__(64) void lse_merge_kernel(const float* __restrict__ part_o,
-                                                       const float* __restrict__ part_lse,
-                                                       uint16_t* __restrict__ out,
-                                                       int num_splits, int n_q) {
+// One workgroup of nw waves per (64 dims of a q head, sequence); wave v folds
+// the splits v, v + nw, v + 2 nw, ... in chunks of MCH: lane j loads the lse
+// of the chunk's split j (one vector load) and lane d the chunk's partials of
+// its dim, the chunk max and weight sum are wave reductions, and lane d folds
+// its partials with the weights broadcast from their lanes (v_readlane).
+// Every load of a chunk is unconditional (indices past the wave's last split
+// are clamped, with uniform scalar arithmetic, and carry no weight), so a
+// chunk costs one round trip; with nw = ceil(num_splits / MCH) waves each
+// wave has a single chunk.  The waves then meet in LDS: the same merge over
+// their (max, weight sum, weighted partial).  Splits with lse = -inf carry no
+// weight; a NaN lse or partial makes the output NaN; no weight at all gives 0.
+constexpr int MCH = 16;        // splits per wave per round trip
+constexpr int MERGE_WAVES = 16;
+
+__global__ __launch_bounds__(64 * MERGE_WAVES) void lse_merge_kernel(
+    const float* __restrict__ part_o, const float* __restrict__ part_lse,
+    uint16_t* __restrict__ out, int num_splits, int n_q, int nw) {
+  __shared__ float m_s[MERGE_WAVES], l_s[MERGE_WAVES], a_s[MERGE_WAVES][64];
+  __shared__ int bad_s[MERGE_WAVES];
   const int h = blockIdx.x >> 1, seq = blockIdx.y;
-  const int lane = threadIdx.x, d = (blockIdx.x & 1) * 64 + lane;
+  const int lane = threadIdx.x & 63, d = (blockIdx.x & 1) * 64 + lane;
+  const int v = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t row = (int64_t)seq * num_splits * n_q + h;  // (seq, split 0, h)
-  const int pstep = n_q * HD;  // n_q <= 65535: 63 steps stay below 2^31
+  const int cnt = v < num_splits ? (num_splits - 1 - v) / nw + 1 : 0;  // this wave's splits
+  const int64_t sstep = (int64_t)nw * n_q;                           // split v -> v + nw
   float m = -INFINITY, l = 0.f, acc = 0.f;
   bool poisoned = false;
-  for (int c0 = 0; c0 < num_splits; c0 += 64) {
-    const int last = num_splits - 1 - c0;  // last valid j of this chunk (uniform)
-    const float lraw = part_lse[row + (int64_t)(c0 + min(lane, last)) * n_q];
-    float pv[64];
-    const float* pp = part_o + (row + (int64_t)c0 * n_q) * HD + d;
-    int off = 0;  // element offset of split c0 + min(j, last): stops at the last split
+  for (int i0 = 0; i0 < cnt; i0 += MCH) {
+    const int last = min(cnt - 1 - i0, MCH - 1);  // last valid j of this chunk (uniform)
+    const int64_t c0 = row + ((int64_t)v + (int64_t)i0 * nw) * n_q;  // split v + nw i0
+    const float lraw = part_lse[c0 + (int64_t)min(lane, last) * sstep];
+    float pv[MCH];
+    const float* pp = part_o + c0 * HD + d;
+    int64_t off = 0;  // element offset of split v + nw (i0 + min(j, last))
 #pragma unroll
-    for (int j = 0; j < 64; ++j) {
+    for (int j = 0; j < MCH; ++j) {
       pv[j] = pp[off];
-      off += j < last ? pstep : 0;
+      off += j < last ? sstep * HD : 0;
     }
     // every load of the chunk is issued before the wait for its lse values
     // (nothing may be scheduled across this point)
@@ -521,15 +530,35 @@ __global__ __launch_bounds__(64) void lse_merge_kernel(const float* __restrict__
     l = l * a + wave_sum(wl);
     acc *= a;
 #pragma unroll
-    for (int j = 0; j < 64; ++j) {
+    for (int j = 0; j < MCH; ++j) {
       const float wj = __builtin_bit_cast(
           float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), j));
       acc = fmaf(wj, pv[j], acc);
     }
     m = mc;
   }
-  const float v = poisoned || acc != acc ? __builtin_nanf("") : (l > 0.f ? acc / l : 0.f);
-  out[((int64_t)seq * n_q + h) * HD + d] = f32_to_bf16(v);
+  if (nw > 1) {
+    a_s[v][lane] = acc;
+    if (lane == 0) {
+      m_s[v] = m;
+      l_s[v] = l;
+      bad_s[v] = poisoned ? 1 : 0;
+    }
+    __syncthreads();
+    if (v != 0) return;
+    float mt = -INFINITY;
+    for (int w = 0; w < nw; ++w) mt = fmaxf(mt, m_s[w]);
+    l = 0.f;
+    acc = 0.f;
+    for (int w = 0; w < nw; ++w) {
+      const float f = m_s[w] == -INFINITY ? 0.f : expf(m_s[w] - mt);
+      l = fmaf(f, l_s[w], l);
+      acc = fmaf(f, a_s[w][lane], acc);
+      poisoned |= bad_s[w] != 0;
+    }
+  }
+  const float r = poisoned || acc != acc ? __builtin_nanf("") : (l > 0.f ? acc / l : 0.f);
+  out[((int64_t)seq * n_q + h) * HD + d] = f32_to_bf16(r);
 }
 
 }  // namespace
@@ -605,9 +634,11 @@ smx::SplitKVArgs splitkv_args(const void* q, const void* k_cache, const void* v_
 
 int launch_merge(void* stream, const float* partial_o, const float* partial_lse, void* out,
                  int32_t num_seqs, int32_t num_splits, int32_t n_q) {
-  hipLaunchKernelGGL(smx::lse_merge_kernel, dim3(2 * n_q, num_seqs), dim3(64), 0,
+  // one chunk per wave where possible (at most MERGE_WAVES waves)
+  const int nw = std::min((num_splits + smx::MCH - 1) / smx::MCH, smx::MERGE_WAVES);
+  hipLaunchKernelGGL(smx::lse_merge_kernel, dim3(2 * n_q, num_seqs), dim3(64 * nw), 0,
                      (hipStream_t)stream, partial_o, partial_lse, (uint16_t*)out, num_splits,
-                     n_q);
+                     n_q, nw);
   return (int)hipGetLastError();
 }
 }  // namespace
