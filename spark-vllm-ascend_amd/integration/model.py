@@ -108,8 +108,9 @@ class DecodeState:
 class DecodeModel:
     """A Q4_0 decoder with random-init weights of a given shape, decoding
     `batch` sequences per step (one token each).  batch == 1 runs the fused
-    GEMV path; batch > 1 runs the MFMA GEMM (m = batch rows) with separate
-    norm launches, over a block table with one row per sequence."""
+    GEMV path; batch > 1 runs the multi-row Q4_0 GEMM (m = batch rows) with
+    separate add+RMSNorm launches and the fused q/k-norm + RoPE + KV-write
+    split-KV kernel, over a block table with one row per sequence."""
 
     def __init__(self, cfg: DecoderConfig, device, seed: int = 0, max_len: int = 8192,
                  num_splits: int | None = None, weights: dict | None = None,
@@ -241,12 +242,10 @@ class DecodeModel:
             B = self.batch
             ops.add_rmsnorm(x_in, r_in, L.input_norm, c.eps, out=self.h, residual_out=self.res_a)
             ops.q4_0_gemm(self.h, L.qkv.qweight, c.qkv_rows, c.hidden, out=self.qkv_out)
-            ops.qknorm_rope_kv_write(self.qkv_out, L.q_norm, L.k_norm, self.cos_sin, st.positions,
-                                     st.slot_mapping, L.kv_cache[0], L.kv_cache[1], c.n_q, c.n_kv,
-                                     c.eps, q_out=self.q)
-            ops.splitkv_decode_merged(self.q, L.kv_cache[0], L.kv_cache[1], st.block_table,
-                                      st.seq_lens, self.num_splits, self.scale, self.partial_o,
-                                      self.partial_lse, out=self.attn)
+            ops.qknorm_rope_splitkv_decode_merged(
+                self.qkv_out, L.q_norm, L.k_norm, self.cos_sin, st.positions, st.slot_mapping,
+                L.kv_cache[0], L.kv_cache[1], st.block_table, st.seq_lens, self.num_splits,
+                self.scale, c.eps, c.n_q, self.partial_o, self.partial_lse, out=self.attn)
             ops.q4_0_gemm(self.attn.view(B, -1), L.o_proj.qweight, c.hidden, c.n_q * c.head_dim,
                           out=self.o)
             ops.add_rmsnorm(self.o, self.res_a, L.post_norm, c.eps, out=self.h2,
