@@ -108,7 +108,7 @@ class DecodeState:
 class DecodeModel:
     """A Q4_0 decoder with random-init weights of a given shape, decoding
     `batch` sequences per step (one token each).  batch == 1 runs the fused
-    GEMV path; batch > 1 runs the multi-row Q4_0 GEMM (m = batch rows) with
+    GEMV path; batch > 1 runs the MFMA Q4_0 GEMM (m = batch rows) with
     separate add+RMSNorm launches and the fused q/k-norm + RoPE + KV-write
     split-KV kernel, over a block table with one row per sequence."""
 

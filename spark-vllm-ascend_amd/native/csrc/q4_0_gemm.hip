@@ -5,21 +5,22 @@
 // -- the GEMV semantics of src/spark_vllm_ascend/kernels/linear.py:16-200 for
 // several rows at once (the reference runs batch 1 only).
 //
-// One workgroup of 8 waves per 16 weight rows (one MFMA N-tile); the waves
-// split the K dimension by block pairs and meet in LDS.  Per block, with
-// v_mfma_f32_16x16x32_bf16 (A = X rows as the M side, B = W^T):
-//  * lane l holds weight row n = l & 15 and k-slot group g = l >> 4: one
-//    32-bit word of the block's nibbles, i.e. 8 weights, which v_perm_b32
-//    turns into bf16 128 + nibble (the nibble spliced under the byte 0x43);
-//  * C = A * B(128 + nibble) + A * B(-136) = sum_k x * (nibble - 8): the
-//    offset is a second MFMA against a constant operand, so no per-block
-//    activation sums are needed;
-//  * the block result is scaled by the lane's row scale d in fp32.
-// The K order inside an MFMA is a permutation shared by A and B: slot j of
-// group g is the element of the word's byte j & 3, low nibble for j < 4 and
-// high nibble (element + 16) otherwise.  Block pairs are 36 bytes, so the
-// even block's nibbles start 2 bytes into a dword; its group-0 word is
-// spliced from the pair's dwords 0 and 4 (elements 14, 15, 0, 1).
+// Both kernels put 16 weight rows x 32 k on one v_mfma_f32_16x16x32_bf16
+// (A = the activation rows as the M side, B = W^T), with the weights as bf16
+// 128 + nibble (v_perm_b32 splices each nibble under the byte 0x43), a second
+// MFMA against a constant -136 operand (C = A.B(128+n) + A.B(-136) = sum x (n - 8),
+// no per-block activation sums) and the block result scaled by the row's fp16
+// d in fp32.
+//  * q4_0_gemm_tile_kernel (16-byte aligned activations): the GEMV's 16-byte
+//    pair loads, redistributed across lanes by permlane swaps (below).
+//  * q4_0_gemm_kernel (8-byte aligned activations): one workgroup of 8 waves
+//    per 16 rows, each lane loading one 32-bit word of a block's nibbles.
+//    A lane holds weight row n = l & 15 and k-slot group g = l >> 4.  The K
+//    order inside an MFMA is a permutation shared by A and B: slot j of group
+//    g is the element of the word's byte j & 3, low nibble for j < 4 and high
+//    nibble (element + 16) otherwise.  Block pairs are 36 bytes, so the even
+//    block's nibbles start 2 bytes into a dword; its group-0 word is spliced
+//    from the pair's dwords 0 and 4 (elements 14, 15, 0, 1).
 #include "smx_common.h"
 
 namespace smx {
@@ -153,18 +154,156 @@ __global__ __launch_bounds__(512) void q4_0_gemm_kernel(GemmArgs a) {
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// The same GEMM with the GEMV's 16-byte weight loads.  Lane l = 16 j + n of
+// a wave reads block pair 4t + j of weight row n (two 16-byte loads and one
+// 4-byte load, as the GEMV); a 4x4 transpose across the lanes n + 16 j
+// (v_permlane16_swap / v_permlane32_swap) then gives lane (n, g) the k-group
+// g of all 8 blocks of the tile: with the k-order of a block chosen as
+// group g = elements 8g..8g+7 (low nibbles of qs[8g..8g+7] for g < 2, high
+// nibbles of qs[8(g-2)..] for g >= 2), each group needs one 8-byte half of
+// a block's qs and the activations of a group are 16 contiguous bytes of x.
+// One v_mfma_f32_16x16x32_bf16 per block (A = activation row n, B = weight
+// row n as bf16 128 + nibble) plus one against the constant -136, scaled by
+// the block's fp16 d in fp32 (the scales travel through the same transpose).
+// The waves of a workgroup take the tiles t = wave, wave + ks, ...
+// ---------------------------------------------------------------------------
+
+// 4x4 transpose across the four 16-lane rows: on entry row j of r_g holds
+// X[j][g]; on exit row g of r_k holds X[k][g].  v_permlane16_swap(a, b)
+// swaps the odd rows of a with the even rows of b; v_permlane32_swap(a, b)
+// swaps rows 2-3 of a with rows 0-1 of b.
+__device__ __forceinline__ void transpose_rows4(uint32_t& r0, uint32_t& r1, uint32_t& r2,
+                                                uint32_t& r3) {
+  const auto a = __builtin_amdgcn_permlane16_swap(r0, r1, false, false);
+  const auto b = __builtin_amdgcn_permlane16_swap(r2, r3, false, false);
+  const auto c = __builtin_amdgcn_permlane32_swap(a[0], b[0], false, false);
+  const auto d = __builtin_amdgcn_permlane32_swap(a[1], b[1], false, false);
+  r0 = c[0];
+  r2 = c[1];
+  r1 = d[0];
+  r3 = d[1];
+}
+
+template <bool SWIGLU>
+__global__ __launch_bounds__(1024) void q4_0_gemm_tile_kernel(
+    const uint8_t* w_, const uint16_t* x_, int npairs, int n_out, int64_t up_offset_rows, int ks,
+    int m, int64_t ldx, uint16_t* y, int64_t ldy) {
+  __shared__ f32x4 red[16][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n = lane & 15, j = lane >> 4;  // j is also the lane's k-group after the transpose
+  int wrow;
+  if constexpr (SWIGLU) {
+    const int f = min((int)blockIdx.x * 8 + (n & 7), n_out - 1);
+    wrow = f + (n >= 8 ? (int)up_offset_rows : 0);
+  } else {
+    wrow = min((int)blockIdx.x * 16 + n, n_out - 1);
+  }
+  const uint8_t* wr = w_ + (int64_t)wrow * npairs * 36;
+  const uint16_t* xr = x_ + (int64_t)min(n, m - 1) * ldx;  // rows >= m only feed unused C rows
+  const int ntiles = (npairs + 3) >> 2;
+  const uint32_t hshift = (uint32_t)(j >> 1) * 4u;  // high nibbles for k-groups 2 and 3
+  bf16x8 bneg;
+  {
+    const uint32_t c[4] = {kNeg136, kNeg136, kNeg136, kNeg136};
+    bneg = __builtin_bit_cast(bf16x8, c);
+  }
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+  f32x4 acc = zero;
+  for (int t = wave; t < ntiles; t += ks) {
+    // this lane's pair (clamped; a pair past the row end gets scale 0)
+    const int pj = 4 * t + j;
+    const uint32_t* pw = reinterpret_cast<const uint32_t*>(wr + 36 * min(pj, npairs - 1));
+    const u32x4 pa = *reinterpret_cast<const u32x4_a4*>(pw);
+    const u32x4 pb = *reinterpret_cast<const u32x4_a4*>(pw + 4);
+    const uint32_t p8 = pw[8];
+    // the activations of the tile's 8 blocks for this lane's row and k-group
+    u32x4 xa[8];
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      const int pp = min(4 * t + (b >> 1), npairs - 1);
+      xa[b] = *reinterpret_cast<const u32x4*>(xr + pp * 64 + (b & 1) * 32 + 8 * j);
+    }
+    // qs dwords of the even block (bytes 2..17 of the pair) and the odd one
+    // (bytes 20..35), and the two scales packed (d_even | d_odd << 16)
+    const uint32_t qe0 = perm_b32(pa.y, pa.x, 0x05040302u);
+    const uint32_t qe1 = perm_b32(pa.z, pa.y, 0x05040302u);
+    const uint32_t qe2 = perm_b32(pa.w, pa.z, 0x05040302u);
+    const uint32_t qe3 = perm_b32(pb.x, pa.w, 0x05040302u);
+    const uint32_t dd = pj < npairs ? perm_b32(pb.x, pa.x, 0x07060100u) : 0u;
+    // k-group g takes the 8-byte half g & 1 of each block's qs
+    uint32_t ea0 = qe0, ea1 = qe2, ea2 = qe0, ea3 = qe2;
+    uint32_t eb0 = qe1, eb1 = qe3, eb2 = qe1, eb3 = qe3;
+    uint32_t oa0 = pb.y, oa1 = pb.w, oa2 = pb.y, oa3 = pb.w;
+    uint32_t ob0 = pb.z, ob1 = p8, ob2 = pb.z, ob3 = p8;
+    uint32_t d0 = dd, d1 = dd, d2 = dd, d3 = dd;
+    transpose_rows4(ea0, ea1, ea2, ea3);
+    transpose_rows4(eb0, eb1, eb2, eb3);
+    transpose_rows4(oa0, oa1, oa2, oa3);
+    transpose_rows4(ob0, ob1, ob2, ob3);
+    transpose_rows4(d0, d1, d2, d3);
+    const uint32_t qa[8] = {ea0, oa0, ea1, oa1, ea2, oa2, ea3, oa3};  // block b = 2k + odd
+    const uint32_t qb[8] = {eb0, ob0, eb1, ob1, eb2, ob2, eb3, ob3};
+    const uint32_t dk[4] = {d0, d1, d2, d3};
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      const uint32_t lo = (qa[b] >> hshift) & kNibG;
+      const uint32_t hi = (qb[b] >> hshift) & kNibG;
+      const uint32_t bw[4] = {perm_b32(kMagicG, lo, kSel01G), perm_b32(kMagicG, lo, kSel23G),
+                              perm_b32(kMagicG, hi, kSel01G), perm_b32(kMagicG, hi, kSel23G)};
+      const bf16x8 A = __builtin_bit_cast(bf16x8, xa[b]);
+      f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, __builtin_bit_cast(bf16x8, bw), zero,
+                                                        0, 0, 0);
+      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, bneg, c, 0, 0, 0);
+      const float d = f16_bits_to_f32((b & 1) ? (dk[b >> 1] >> 16) : (dk[b >> 1] & 0xffffu));
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[r] = fmaf(d, c[r], acc[r]);
+    }
+  }
+  // C layout: lane l holds rows 4 (l >> 4) + r of column l & 15.
+  red[wave][lane] = acc;
+  __syncthreads();
+  for (int e = threadIdx.x; e < 256; e += 64 * ks) {  // 16 rows x 16 columns
+    const int mr = e >> 4, nn = e & 15;
+    auto total = [&](int col) {
+      float s = 0.f;
+      for (int w = 0; w < ks; ++w) s += red[w][16 * (mr >> 2) + col][mr & 3];
+      return s;
+    };
+    if (mr < m) {
+      if constexpr (SWIGLU) {
+        const int f = blockIdx.x * 8 + nn;
+        if (nn < 8 && f < n_out) {
+          const float gb = round_bf16(total(nn));
+          const float ub = round_bf16(total(nn + 8));
+          y[(int64_t)mr * ldy + f] = f32_to_bf16(gb / (1.0f + expf(-gb)) * ub);
+        }
+      } else {
+        const int o = blockIdx.x * 16 + nn;
+        if (o < n_out) y[(int64_t)mr * ldy + o] = f32_to_bf16(total(nn));
+      }
+    }
+  }
+}
+
+template <bool SWIGLU>
+hipError_t launch_gemm_tile(hipStream_t s, const void* x, const void* w, void* y, int64_t m,
+                            int64_t n_out, int64_t k, int64_t up_offset_rows) {
+  const int npairs = (int)(k / 64);
+  const int ntiles = (npairs + 3) / 4;
+  const int ks = ntiles < 16 ? ntiles : 16;
+  const int grid = SWIGLU ? (int)((n_out + 7) / 8) : (int)((n_out + 15) / 16);
+  hipLaunchKernelGGL(q4_0_gemm_tile_kernel<SWIGLU>, dim3(grid), dim3(64 * ks), 0, s,
+                     (const uint8_t*)w, (const uint16_t*)x, npairs, (int)n_out, up_offset_rows, ks,
+                     (int)m, k, (uint16_t*)y, n_out);
+  return hipGetLastError();
+}
 }  // namespace
 }  // namespace smx
 
 #include "smx_abi_util.h"
 
-namespace smx {
-// Multi-row streaming GEMV (q4_0_gemv.hip); hipErrorNotSupported for shapes
-// it does not take (then the MFMA kernel above runs).
-hipError_t q4_0_gemv_rows(hipStream_t s, const void* x, const void* w, void* y, int64_t m,
-                          int64_t n_out, int64_t k, int64_t ldx, int64_t ldy, bool swiglu,
-                          int64_t up_offset_rows);
-}  // namespace smx
 
 #define SMX_GEMM_CHECKS(N)                                                                      \
   SMX_REQUIRE(x && w && y, "null pointer argument");                                            \
@@ -177,10 +316,8 @@ hipError_t q4_0_gemv_rows(hipStream_t s, const void* x, const void* w, void* y, 
 extern "C" int smx_q4_0_gemm(void* stream, const void* x, const void* w, void* y, int64_t m,
                              int64_t n, int64_t k) {
   SMX_GEMM_CHECKS(n);
-  {
-    const hipError_t e = smx::q4_0_gemv_rows((hipStream_t)stream, x, w, y, m, n, k, k, n, false, 0);
-    if (e != hipErrorNotSupported) return (int)e;
-  }
+  if ((uintptr_t)x % 16 == 0)
+    return (int)smx::launch_gemm_tile<false>((hipStream_t)stream, x, w, y, m, n, k, 0);
   smx::GemmArgs a{(const uint16_t*)x, (const uint8_t*)w, (uint16_t*)y, (int)m, (int)n,
                   (int)(k / 64), k, n, 0};
   hipLaunchKernelGGL(smx::q4_0_gemm_kernel<false>, dim3((unsigned)((n + 15) / 16)), dim3(512), 0,
@@ -191,10 +328,8 @@ extern "C" int smx_q4_0_gemm(void* stream, const void* x, const void* w, void* y
 extern "C" int smx_q4_0_gemm_swiglu(void* stream, const void* x, const void* w, void* y,
                                     int64_t m, int64_t d, int64_t k) {
   SMX_GEMM_CHECKS(d);
-  {
-    const hipError_t e = smx::q4_0_gemv_rows((hipStream_t)stream, x, w, y, m, d, k, k, d, true, d);
-    if (e != hipErrorNotSupported) return (int)e;
-  }
+  if ((uintptr_t)x % 16 == 0)
+    return (int)smx::launch_gemm_tile<true>((hipStream_t)stream, x, w, y, m, d, k, d);
   smx::GemmArgs a{(const uint16_t*)x, (const uint8_t*)w, (uint16_t*)y, (int)m, (int)d,
                   (int)(k / 64), k, d, d};
   hipLaunchKernelGGL(smx::q4_0_gemm_kernel<true>, dim3((unsigned)((d + 7) / 8)), dim3(512), 0,

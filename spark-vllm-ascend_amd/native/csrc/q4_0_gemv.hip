@@ -417,180 +417,6 @@ __global__ __launch_bounds__(256) void q4_0_dequant_kernel(
   }
 }
 
-// ---------------------------------------------------------------------------
-// The same weight stream for a few activation rows (batched decode, m <= MM):
-// y[r][o] = sum_k x[r][k] * W[o][k].  The lane / wave / workgroup layout and
-// the weight loads are the GEMV's; each lane dequantises its block pairs
-// ONCE into registers (the bf16 pairs 128 + nibble that the GEMV builds per
-// word with v_perm_b32) and then, row by row, stages that row's activation
-// slice in its wave's private LDS (as the GEMV does: no cross-wave barrier)
-// and accumulates 32 v_dot2 per pair.  All activation rows are loaded with
-// the weights, up front.  The -136 * sum(x) block bias and the fp32 scaling
-// by d are the GEMV's, per row.
-// ---------------------------------------------------------------------------
-
-// The 32 bf16 pairs (128 + nibble) of a block pair, in pair_dot's word
-// order: e0 (qs 14,15,0,1 of the even block), a.y, a.z, a.w, b.y, b.z, b.w, c,
-// each as perm(l, 01), perm(l, 23), perm(h, 01), perm(h, 23).
-struct PairDq {
-  uint32_t v[32];
-  float de, dd;
-};
-
-__device__ __forceinline__ void dequant_pair(const Pair& w, PairDq& q) {
-  const uint32_t words[8] = {(w.a.x & 0xffff0000u) | (w.b.x & 0x0000ffffu), w.a.y, w.a.z, w.a.w,
-                             w.b.y, w.b.z, w.b.w, w.c};
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const uint32_t l = words[i] & kNib;
-    const uint32_t h = (words[i] >> 4) & kNib;
-    q.v[4 * i + 0] = perm_b32(kMagic, l, kSel01);
-    q.v[4 * i + 1] = perm_b32(kMagic, l, kSel23);
-    q.v[4 * i + 2] = perm_b32(kMagic, h, kSel01);
-    q.v[4 * i + 3] = perm_b32(kMagic, h, kSel23);
-  }
-  q.de = f16_bits_to_f32(w.a.x & 0xffffu);
-  q.dd = f16_bits_to_f32(w.b.x >> 16);
-}
-
-// pair_dot on a dequantised pair (same products, same order).
-__device__ __forceinline__ float pair_dot_dq(const PairDq& q, const u32x4* xs, float acc) {
-  const u32x4 x0 = xs[0], x1 = xs[1], x2 = xs[2], x3 = xs[3];
-  const u32x4 y0 = xs[4], y1 = xs[5], y2 = xs[6], y3 = xs[7];
-  const u32x2 bias = *reinterpret_cast<const u32x2*>(xs + 8);
-  const uint32_t xe[8][4] = {{x1.w, x0.x, x3.w, x2.x}, {x0.y, x0.z, x2.y, x2.z},
-                             {x0.w, x1.x, x2.w, x3.x}, {x1.y, x1.z, x3.y, x3.z}};
-  const uint32_t xo[4][4] = {{y0.x, y0.y, y2.x, y2.y}, {y0.z, y0.w, y2.z, y2.w},
-                             {y1.x, y1.y, y3.x, y3.y}, {y1.z, y1.w, y3.z, y3.w}};
-  float se = __uint_as_float(bias.x), so = __uint_as_float(bias.y);
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) se = dot2_bf16(q.v[4 * i + j], xe[i][j], se);
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) so = dot2_bf16(q.v[16 + 4 * i + j], xo[i][j], so);
-  acc = fmaf(q.de, se, acc);
-  return fmaf(q.dd, so, acc);
-}
-
-struct RowsTail {
-  uint16_t* y;  // [m, ldy] bf16
-  int64_t ldy;
-};
-
-// Leading scalar / pointer arguments are preloaded (see GemvTail).
-template <int NPMAX, int RG, int MM, bool SWIGLU>
-__global__ __launch_bounds__(NPMAX <= 1 ? 1024 : 640) void q4_0_gemv_rows_kernel(
-    const uint8_t* w_, const uint16_t* x_, int npairs, int n_out, int64_t up_offset_rows, int ks,
-    int m, int64_t ldx, RowsTail tail) {
-  extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int col = lane & 7, rsub = lane >> 3;
-  const int64_t row_bytes = (int64_t)npairs * 36;
-  const int nchunks = npairs * 8;
-  uint32_t* xs = lds + wave * (NPMAX * 8 * 36);
-  float* part = reinterpret_cast<float*>(lds + ks * (NPMAX * 8 * 36));
-
-  // 1. every activation chunk of every row, then every weight load (clamped
-  //    addresses, masked afterwards, as in the GEMV)
-  u32x4 xv[MM][NPMAX];
-#pragma unroll
-  for (int r = 0; r < MM; ++r) {
-    const u32x4* xg = reinterpret_cast<const u32x4*>(x_ + (int64_t)min(r, m - 1) * ldx);
-#pragma unroll
-    for (int t = 0; t < NPMAX; ++t) xv[r][t] = xg[min((wave + ks * t) * 64 + lane, nchunks - 1)];
-  }
-  constexpr int OUT_PER_GROUP = SWIGLU ? 4 : 8;
-  Pair wp[RG][NPMAX];
-#pragma unroll
-  for (int g = 0; g < RG; ++g) {
-    const int o = (blockIdx.x * RG + g) * OUT_PER_GROUP + (SWIGLU ? (rsub & 3) : rsub);
-    const int oc = min(o, n_out - 1);
-    const int64_t wrow = SWIGLU ? (oc + ((rsub >> 2) ? up_offset_rows : 0)) : oc;
-#pragma unroll
-    for (int t = 0; t < NPMAX; ++t) {
-      const int j = min((wave + ks * t) * 8 + col, npairs - 1);
-      wp[g][t] = load_pair(w_ + wrow * row_bytes + 36 * j);
-    }
-  }
-  // 2. dequantise each pair once
-  PairDq dq[RG][NPMAX];
-#pragma unroll
-  for (int g = 0; g < RG; ++g)
-#pragma unroll
-    for (int t = 0; t < NPMAX; ++t) dequant_pair(wp[g][t], dq[g][t]);
-
-  // 3. row by row: stage the row's activation slice, then the dot products
-  float acc[RG][MM];
-#pragma unroll
-  for (int r = 0; r < MM; ++r) {
-#pragma unroll
-    for (int g = 0; g < RG; ++g) acc[g][r] = 0.f;
-#pragma unroll
-    for (int t = 0; t < NPMAX; ++t) {
-      const bool ok = (wave + ks * t) * 64 + lane < nchunks;
-      const u32x4 v = ok ? xv[r][t] : u32x4{0u, 0u, 0u, 0u};
-      float sb = 0.f;
-      sb = dot2_bf16(v.x, kOnes, sb);
-      sb = dot2_bf16(v.y, kOnes, sb);
-      sb = dot2_bf16(v.z, kOnes, sb);
-      sb = dot2_bf16(v.w, kOnes, sb);
-      sb = sum4(sb);
-      uint32_t* rec = xs + (t * 8 + (lane >> 3)) * 36;
-      *reinterpret_cast<u32x4*>(rec + 4 * (lane & 7)) = v;
-      if ((lane & 3) == 0) rec[32 + ((lane >> 2) & 1)] = __float_as_uint(-136.0f * sb);
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-    for (int t = 0; t < NPMAX; ++t) {
-      const int j = (wave + ks * t) * 8 + col;
-      if (j < npairs) {
-        const u32x4* rec = reinterpret_cast<const u32x4*>(xs + (t * 8 + col) * 36);
-#pragma unroll
-        for (int g = 0; g < RG; ++g) acc[g][r] = pair_dot_dq(dq[g][t], rec, acc[g][r]);
-      }
-    }
-    // the next row overwrites the slice: this wave's reads of it come first
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  }
-
-  // 4. row sums: 8 lanes by DPP, then the ks waves through LDS
-#pragma unroll
-  for (int g = 0; g < RG; ++g)
-#pragma unroll
-    for (int r = 0; r < MM; ++r) {
-      const float v = sum8(acc[g][r]);
-      if (col == 0) part[((wave * RG + g) * 8 + rsub) * MM + r] = v;
-    }
-  __syncthreads();
-  for (int e = tid; e < RG * 8 * MM; e += blockDim.x) {
-    const int r = e % MM, rs = (e / MM) % 8, g = e / (8 * MM);
-    if (r >= m) continue;
-    auto total = [&](int rr) {
-      float s = 0.f;
-      for (int i = 0; i < ks; ++i) s += part[((i * RG + g) * 8 + rr) * MM + r];
-      return s;
-    };
-    if constexpr (SWIGLU) {
-      const int o = (blockIdx.x * RG + g) * 4 + rs;
-      if (rs < 4 && o < n_out) {
-        const float gb = round_bf16(total(rs));
-        const float ub = round_bf16(total(rs + 4));
-        tail.y[(int64_t)r * tail.ldy + o] = f32_to_bf16(gb / (1.0f + expf(-gb)) * ub);
-      }
-    } else {
-      const int o = (blockIdx.x * RG + g) * 8 + rs;
-      if (o < n_out) tail.y[(int64_t)r * tail.ldy + o] = f32_to_bf16(total(rs));
-    }
-  }
-}
-
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -731,51 +557,6 @@ static hipError_t gemv_dispatch(hipStream_t s, GemvArgs a, int64_t k, int epi, b
   if (epi == EPI_SWIGLU) return dispatch_np<false, EPI_SWIGLU>(s, a, sh);
   if (epi == EPI_ARGMAX) return dispatch_np<false, EPI_ARGMAX>(s, a, sh);
   return dispatch_np<false, EPI_STORE>(s, a, sh);
-}
-
-// Multi-row GEMV (batched decode): one row group of 8 weight rows per
-// workgroup (the dequantised pairs live in registers), one or two pair
-// groups per wave, at most 10 waves; rows in chunks of MM.
-template <int NPMAX, int MM, bool SWIGLU>
-static hipError_t launch_rows(hipStream_t s, const uint8_t* w, const uint16_t* x, uint16_t* y,
-                              int m, int n_out, int npairs, int ks, int64_t ldx, int64_t ldy,
-                              int64_t up_offset_rows) {
-  constexpr int OUT_PER_WG = SWIGLU ? 4 : 8;
-  const int grid = (n_out + OUT_PER_WG - 1) / OUT_PER_WG;
-  const size_t lds = (size_t)ks * NPMAX * 8 * 36 * 4 + (size_t)ks * 8 * MM * 4;
-  hipLaunchKernelGGL((q4_0_gemv_rows_kernel<NPMAX, 1, MM, SWIGLU>), dim3(grid), dim3(64 * ks), lds,
-                     s, w, x, npairs, n_out, up_offset_rows, ks, m, ldx, RowsTail{y, ldy});
-  return hipGetLastError();
-}
-
-template <int MM, bool SWIGLU>
-static hipError_t rows_np(hipStream_t s, const uint8_t* w, const uint16_t* x, uint16_t* y, int m,
-                          int n_out, int npairs, int64_t ldx, int64_t ldy, int64_t up) {
-  const int ngroups = (npairs + 7) / 8;
-  if (ngroups <= 16) return launch_rows<1, MM, SWIGLU>(s, w, x, y, m, n_out, npairs, ngroups, ldx, ldy, up);
-  const int ks = (ngroups + 1) / 2;
-  return launch_rows<2, MM, SWIGLU>(s, w, x, y, m, n_out, npairs, ks, ldx, ldy, up);
-}
-
-// Returns hipErrorNotSupported for shapes the multi-row kernel does not take.
-hipError_t q4_0_gemv_rows(hipStream_t s, const void* x, const void* w, void* y, int64_t m,
-                          int64_t n_out, int64_t k, int64_t ldx, int64_t ldy, bool swiglu,
-                          int64_t up_offset_rows) {
-  if (m < 1 || m > 8 || k % 64 != 0 || k > 20 * 512 || (uintptr_t)w % 4 != 0 ||
-      (uintptr_t)x % 16 != 0 || (ldx * 2) % 16 != 0)
-    return hipErrorNotSupported;
-  const int npairs = (int)(k / 64);
-  const uint8_t* wb = (const uint8_t*)w;
-  const uint16_t* xb = (const uint16_t*)x;
-  uint16_t* yb = (uint16_t*)y;
-  const int mi = (int)m, n = (int)n_out;
-#define SMX_ROWS(MM)                                                                            \
-  return swiglu ? rows_np<MM, true>(s, wb, xb, yb, mi, n, npairs, ldx, ldy, up_offset_rows)    \
-                : rows_np<MM, false>(s, wb, xb, yb, mi, n, npairs, ldx, ldy, up_offset_rows)
-  if (m <= 2) SMX_ROWS(2);
-  if (m <= 4) SMX_ROWS(4);
-  SMX_ROWS(8);
-#undef SMX_ROWS
 }
 
 }  // namespace smx

@@ -1,5 +1,5 @@
-"""GPU parity of the batched Q4_0 GEMM (streaming multi-row kernel for up to
-8 rows, MFMA above) through the C ABI: each output
+"""GPU parity of the batched Q4_0 GEMM (MFMA tile kernel over the GEMV's
+16-byte pair loads, up to 16 rows) through the C ABI: each output
 row within 1e-2 relative of the float64 oracle GEMV of that activation row;
 one-hot activations select dequantised weights bit-exactly (this pins the
 MFMA operand and result layouts); SwiGLU epilogue; writes stay in bounds."""
@@ -48,9 +48,9 @@ def test_gemm_vs_oracle(ops, dev, m, n, k):
 @pytest.mark.parametrize("m", [3, 8, 16])
 def test_gemm_one_hot_layout(ops, dev, m):
     """Row m of x is one-hot at column c_m: y[m][n] = bf16(dequant(W)[n][c_m])
-    exactly, for up to 16 rows (m <= 8: the streaming multi-row kernel, else
-    the MFMA kernel), 48 output rows and columns spread over both blocks of a
-    pair and all nibble positions."""
+    exactly, for up to 16 rows, 48 output rows and columns spread over both
+    blocks of a pair and all nibble positions (this pins the permlane
+    transpose and the MFMA operand and result layouts)."""
     n, k = 48, 256
     blocks = oq.make_blocks(n, k, seed=11, scale=1.0)
     cols = np.array([0, 1, 14, 15, 16, 17, 30, 31, 32, 33, 46, 47, 48, 63, 100, 255])[:m]
@@ -73,6 +73,35 @@ def test_gemm_swiglu(ops, dev, m, d, k):
         g = bf16_bits_to_f32(f32_to_bf16_bits(gu[:d]))
         u = bf16_bits_to_f32(f32_to_bf16_bits(gu[d:]))
         assert_close_rel(out[r], o_silu_mul(g, u), rtol=2e-2, atol_frac=5e-3, what=f"row {r}")
+
+
+@pytest.mark.parametrize("m", [2, 8])
+@pytest.mark.parametrize("swiglu", [False, True])
+def test_gemm_8_byte_aligned_activations(ops, dev, m, swiglu):
+    """Activations that are 8- but not 16-byte aligned take the word-load
+    MFMA kernel: same oracle bound as the tile kernel."""
+    import torch
+    n, k = 96, 512
+    rng = np.random.default_rng(m + 10 * swiglu)
+    blocks = oq.make_blocks(2 * n if swiglu else n, k, seed=m + 3)
+    x = randn_bf16(rng, (m, k))
+    buf = torch.empty(m * k + 8, dtype=torch.bfloat16, device=dev)
+    xv = buf[4:4 + m * k].view(m, k)  # 8 bytes past a 16-byte aligned allocation
+    assert xv.data_ptr() % 16 == 8
+    xv.copy_(bf16_dev(x, dev))
+    if swiglu:
+        out = f32_of(ops.q4_0_gemm_swiglu(xv, _w(blocks, dev), n, k)).reshape(m, n)
+    else:
+        out = f32_of(ops.q4_0_gemm(xv, _w(blocks, dev), n, k)).reshape(m, n)
+    for r in range(m):
+        if swiglu:
+            gu = oq.gemv_f64(x[r], blocks, 2 * n, k).astype(np.float32)
+            ref = o_silu_mul(bf16_bits_to_f32(f32_to_bf16_bits(gu[:n])),
+                             bf16_bits_to_f32(f32_to_bf16_bits(gu[n:])))
+            assert_close_rel(out[r], ref, rtol=2e-2, atol_frac=5e-3, what=f"row {r}")
+        else:
+            assert_close_rel(out[r], oq.gemv_f64(x[r], blocks, n, k), rtol=1e-2, atol_frac=5e-3,
+                             what=f"row {r}")
 
 
 def test_gemm_output_sentinels(ops, dev):
