@@ -37,16 +37,22 @@ class SplitKVDecodeMetadata:
     max_seq_len: int = 0          # host hint used only to choose num_splits
 
 
-def choose_num_splits(capacity: int, tokens_per_split: int = 128) -> int:
+def choose_num_splits(capacity: int, tokens_per_split: int = 128, num_seqs: int = 1) -> int:
     """Split count for a block table addressing `capacity` tokens.  Splits
     are cut from the capacity (not the current length), so one captured graph
-    serves every step.  Measured on MI355X: 128 tokens per split (four waves
-    of one 32-token block each, two workgroups per CU) is best for one
-    sequence at 2k..6k (49 splits at a 6272-token capacity; 32 or 33 splits
-    of 224 / 192 tokens put one 8-wave workgroup on a CU, and past 256
-    workgroups the rest run in a second round) and for 8 sequences at
-    6k..31k."""
-    return int(max(1, -(-capacity // tokens_per_split)))
+    serves every step.  Measured on MI355X:
+      * one sequence: 128 tokens per split (four waves of one 32-token block
+        each, two workgroups per CU) is best at 2k..6k (49 splits at a
+        6272-token capacity; 32 or 33 splits of 224 / 192 tokens put one
+        8-wave workgroup on a CU, and past 256 workgroups the rest run in a
+        second round);
+      * several sequences: about 25 long splits whatever the capacity (8
+        sequences at 512..32768 tokens, 32896-token capacity: 25 splits of
+        1344 tokens 5.47 ms per step, 17 / 33 splits 5.52 / 5.56 ms, 257
+        splits of 128 tokens 6.14 ms): the KV stream is large, so fewer
+        workgroups, partials and merge inputs win."""
+    n = int(max(1, -(-capacity // tokens_per_split)))
+    return min(n, 25) if num_seqs > 1 else n
 
 
 class SplitKVDecodeImpl:

@@ -160,7 +160,8 @@ class DecodeModel:
         self.head = TiedQ4_0Head(head_blocks.to(self.device), c.vocab, c.hidden)
         self.cos_sin = rope_cos_sin_cache(max_len, c.head_dim, c.rope_theta, self.device)
         self.scale = 1.0 / math.sqrt(c.head_dim)
-        self.num_splits = num_splits or choose_num_splits(blocks_per_seq * c.block_size)
+        self.num_splits = num_splits or choose_num_splits(blocks_per_seq * c.block_size,
+                                                          num_seqs=B)
 
         # pages are handed out in a seeded shuffled order, to exercise paging
         perm = torch.randperm(self.num_blocks, generator=torch.Generator().manual_seed(seed))
