@@ -116,6 +116,22 @@ def test_argmax(ops, dev):
     assert out[2] == 1234
 
 
+def test_argmax_ragged_vocab(ops, dev):
+    """vocab 1003: row 0 is 16-byte aligned (chunks of 8 values, then a
+    3-element tail), the other rows are not (element by element)."""
+    rng = np.random.default_rng(9)
+    v = 1003
+    logits = randn_bf16(rng, (5, v))
+    big = f32_to_bf16_bits(np.float32([50.0]))[0]
+    logits[0, 1001] = big                     # in the tail
+    logits[1, 3] = logits[1, 1002] = big      # tie across rows' elements -> lowest index
+    logits[2, 999] = logits[2, 1000] = big    # tie across the chunk / tail boundary
+    logits[3, 0] = 0x7FC0                     # NaN first element
+    out = ops.argmax(bf16_dev(logits, dev)).cpu().numpy()
+    assert out.tolist()[:4] == [1001, 3, 999, 0]
+    assert out[4] == np.argmax(bf16_bits_to_f32(logits[4]))
+
+
 def test_decode_advance(ops, dev):
     import torch
     table = torch.tensor([[3, 9, 4], [7, 1, 2]], dtype=torch.int32, device=dev)
