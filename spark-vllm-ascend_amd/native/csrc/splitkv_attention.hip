@@ -155,6 +155,13 @@ __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(
       if (lane == 5 || lane == 6)
         src = reinterpret_cast<const uint32_t*>(A.slot_mapping + seq) + (lane - 5);
     }
+    // lanes 8..63: the pages of the wave's chunk from the first one on, so
+    // a wave that walks several blocks looks their pages up with v_readlane
+    // instead of a scalar-load round trip per block
+    if (lane >= 8) {
+      const int pg = (w0 < cap ? (w0 >> bs_log2) : 0) + (lane - 8);
+      src = reinterpret_cast<const uint32_t*>(bt + min(pg, max_blocks - 1));
+    }
     gv = *src;
   }
   // FUSEQ: this workgroup's q heads and the new token's k/v from the raw QKV
@@ -242,10 +249,17 @@ __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(
   //    whole 256-byte rows per load.
   constexpr int NT16 = BLK / 16, NS32 = BLK / 32;
   u32x4 kr[NT16][4], vr[NS32][8];
+  // page of token t >= w0: gathered at entry for the first 56 pages of the
+  // chunk (lanes 8..63), else a block-table load
+  const int pg0 = w0 < cap ? (w0 >> bs_log2) : 0;
+  auto page_of = [&](int t) -> int {
+    const int li = (t >> bs_log2) - pg0 + 8;
+    return li < 64 ? (int)lane_u32(li) : bt[t >> bs_log2];
+  };
   auto load_block = [&](int t0) {
-    const int64_t b0 = half_base(t0, t0 == w0 ? bt0 : bt[t0 >> bs_log2]);
+    const int64_t b0 = half_base(t0, t0 == w0 ? bt0 : page_of(t0));
     const int64_t b1 = BLK == 64 && t0 + 32 < w1
-                           ? half_base(t0 + 32, t0 == w0 ? bt1 : bt[(t0 + 32) >> bs_log2])
+                           ? half_base(t0 + 32, t0 == w0 ? bt1 : page_of(t0 + 32))
                            : b0;
     auto tok_off = [&](int t) -> int64_t {
       const int te = t0 + t < w1 ? t : 0;

@@ -100,6 +100,21 @@ def test_block_sizes(ops, dev, bs):
     assert np.max(np.abs(out.reshape(N_Q, HD) - ref)) < 2e-2
 
 
+@pytest.mark.parametrize("L,bs,splits", [(20000, 32, 1), (9000, 128, 1), (3000, 32, 2)])
+def test_long_wave_chunks(ops, dev, L, bs, splits):
+    """Waves that walk many blocks: their pages come from the entry gather
+    (56 pages per wave) and, past that, from the block table (L=20000 with
+    32-token pages and one split: 2500 tokens = 79 pages per wave)."""
+    rng = np.random.default_rng(L + bs)
+    q, kc, vc, table = _case(rng, [L], bs)
+    scale = HD ** -0.5
+    out, _, _ = _run(ops, dev, q, kc, vc, table, [L], splits, scale)
+    qf, kf, vf = (bf16_bits_to_f32(a) for a in (q, kc, vc))
+    ref = oatt.attention_f64(qf[0], oatt.gather_paged(kf, table[0], L),
+                             oatt.gather_paged(vf, table[0], L), scale)
+    assert np.max(np.abs(out.reshape(N_Q, HD) - ref)) < 2e-2
+
+
 @pytest.mark.parametrize("merged", [False, True])
 def test_ragged_batch(ops, dev, merged):
     rng = np.random.default_rng(5)
