@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define SMX_ABI_VERSION 2
+#define SMX_ABI_VERSION 3
 
 /* Return codes besides 0 and hipError_t values. */
 #define SMX_EINVAL 10001      /* an argument failed validation */
@@ -188,6 +188,64 @@ int smx_qknorm_rope_splitkv_decode_merged(
     int32_t num_seqs, int32_t num_splits, int32_t max_blocks,
     int32_t num_blocks, int32_t block_size, int32_t n_q, int32_t n_kv,
     int32_t head_dim, int32_t max_position, float eps, float scale);
+
+/*
+ * Per-sequence split plan for a batch of decode sequences, computed on the
+ * device from the live lengths (one launch per decode step; every layer's
+ * planned attention reads the same plan).  With L_r = min(seq_lens[r], C),
+ * T = sum_r L_r and
+ *   chunk = 128 * ceil(max(ceil(T / num_items),
+ *                          ceil(max_r L_r / num_splits), 1) / 128),
+ * sequence r gets n_r = ceil(L_r / chunk) <= num_splits splits; split j
+ * covers tokens [j*chunk, min(L_r, (j+1)*chunk)).  The splits are numbered
+ * sequence by sequence and described by plan records (a record per split,
+ * unused records past the last one), at most num_items + num_seqs of them:
+ *   plan: [num_items + num_seqs, SMX_SPLITKV_PLAN_WORDS] uint32
+ *   partial_o [num_seqs, num_splits, n_q, head_dim] fp32 (16-byte aligned),
+ *   partial_lse [num_seqs, num_splits, n_q] fp32: the slots (r, j >= n_r),
+ *     which no split writes, are set to 0 / -inf here, so pass the same
+ *     buffers to the planned attention calls that use this plan.
+ * positions / slot_mapping ([num_seqs] int64) may be NULL unless the plan
+ * feeds smx_qknorm_rope_splitkv_decode_planned_merged.  num_seqs <= 64.
+ * Counterpart of execute_serial's device-side task list, parts =
+ * ceil(length / width) from the live length (src/spark_vllm_ascend/kernels/
+ * attention.py:120-128), with the splits balanced across the batch.
+ */
+#define SMX_SPLITKV_PLAN_WORDS 64
+int smx_splitkv_plan(void* stream, const int32_t* seq_lens, const int64_t* positions,
+                     const int64_t* slot_mapping, const int32_t* block_table,
+                     uint32_t* plan, float* partial_o, float* partial_lse,
+                     int32_t num_seqs, int32_t num_items, int32_t num_splits,
+                     int32_t max_blocks, int32_t block_size, int32_t n_q,
+                     int32_t head_dim);
+
+/*
+ * smx_splitkv_decode_merged over the splits of a plan (smx_splitkv_plan
+ * with the same num_seqs, num_items, num_splits, block table and partial
+ * buffers, enqueued earlier on the stream).  The partials are those of the
+ * plan's splits, with the semantics of smx_splitkv_decode.
+ */
+int smx_splitkv_decode_planned_merged(
+    void* stream, const void* q, const void* k_cache, const void* v_cache,
+    const int32_t* block_table, const uint32_t* plan, float* partial_o,
+    float* partial_lse, void* out, int32_t num_seqs, int32_t num_items,
+    int32_t num_splits, int32_t max_blocks, int32_t num_blocks,
+    int32_t block_size, int32_t n_q, int32_t n_kv, int32_t head_dim,
+    float scale);
+
+/*
+ * smx_qknorm_rope_splitkv_decode_merged over the splits of a plan; the
+ * positions and slots come from the plan (smx_splitkv_plan must have been
+ * given them).
+ */
+int smx_qknorm_rope_splitkv_decode_planned_merged(
+    void* stream, const void* qkv, const void* q_gamma, const void* k_gamma,
+    const void* cos_sin, void* k_cache, void* v_cache,
+    const int32_t* block_table, const uint32_t* plan, float* partial_o,
+    float* partial_lse, void* out, int32_t num_seqs, int32_t num_items,
+    int32_t num_splits, int32_t max_blocks, int32_t num_blocks,
+    int32_t block_size, int32_t n_q, int32_t n_kv, int32_t head_dim,
+    int32_t max_position, float eps, float scale);
 
 /*
  * Log-sum-exp merge of the split partials:

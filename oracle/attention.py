@@ -10,12 +10,21 @@ splitkv_partials  the reference's split-KV online softmax, AttentionStage
 lse_merge         merge_attention (src/spark_vllm_ascend/kernels/vector.py:
                   45-83) without the output gate: w_s = exp(lse_s - max) /
                   sum, out = bf16(sum_s w_s o_s).
+plan_splits       per-sequence splits from the live lengths (the task list
+                  of execute_serial, src/spark_vllm_ascend/kernels/
+                  attention.py:120-128: parts = ceil(length / width)), one
+                  split length for the whole batch; plan_records lays them
+                  out as the device plan's records.
 
 Pins (tests/test_oracle_attention.py): split results merged equal the
 unsplit fp64 result for every split count; one split equals the unsplit
 result; ctx = 1 gives v_0; equal keys give the mean of V; permuting pages
 through the block table leaves the result unchanged; a partially filled last
-page masks its tail.
+page masks its tail.  Plans: every sequence's splits tile [0, L) exactly, no
+sequence has more than num_splits splits, the batch at most num_items +
+num_seqs, the split length is the smallest multiple of 128 meeting both
+bounds (checked by brute force over the multiples), and the merged planned
+partials equal the unsplit fp64 result.
 """
 from __future__ import annotations
 
@@ -107,3 +116,54 @@ def splitkv_decode(q, k_cache, v_cache, table, length, num_splits, scale, tile=1
     cap = len(table) * k_cache.shape[1]
     po, pl = splitkv_partials(q, k, v, scale, split_bounds(length, num_splits, cap), tile)
     return lse_merge(po, pl), po, pl
+
+
+PLAN_WORDS = 64   # uint32 words per plan record
+PLAN_PAGE0 = 9    # record words 9..63: pages from the split's first token on
+PLAN_ALIGN = 128  # split lengths are multiples of this
+
+
+def plan_splits(lengths, num_items: int, num_splits: int, capacity: int,
+                align: int = PLAN_ALIGN):
+    """One split length for the batch,
+    chunk = align * ceil(max(ceil(T / num_items), ceil(max L / num_splits), 1) / align)
+    with L = min(length, capacity) and T = sum L; sequence r gets the splits
+    [j chunk, min(L_r, (j + 1) chunk)) for j < ceil(L_r / chunk).
+    Returns (chunk, [[(begin, end), ...] per sequence])."""
+    L = [min(max(int(x), 0), capacity) for x in lengths]
+    total, lmax = sum(L), max(L)
+    chunk = max(-(-total // num_items), -(-lmax // num_splits), 1)
+    chunk = -(-chunk // align) * align
+    return chunk, [[(j * chunk, min(l, (j + 1) * chunk)) for j in range(-(-l // chunk))]
+                   for l in L]
+
+
+def plan_records(lengths, num_items: int, num_splits: int, table: np.ndarray, block_size: int,
+                 positions=None, slots=None) -> np.ndarray:
+    """The plan's records, [num_items + num_seqs, PLAN_WORDS] uint32: per
+    split (numbered sequence by sequence) the sequence, first / end token,
+    split index, length, position and slot (int64 as two little-endian
+    words; 0 and -1 when not given) and the block-table entries from the
+    first token's page on (indices clamped to the table row); past the last
+    split, records with sequence -1 and zeros."""
+    table = np.asarray(table)
+    cap = table.shape[1] * block_size
+    _, splits = plan_splits(lengths, num_items, num_splits, cap)
+    nrec = num_items + len(lengths)
+    rec = np.zeros((nrec, PLAN_WORDS), dtype=np.uint32)
+    rec[:, 0] = 0xFFFFFFFF
+    b = 0
+    for r, sp in enumerate(splits):
+        L = min(max(int(lengths[r]), 0), cap)
+        p = int(positions[r]) if positions is not None else 0
+        s = int(slots[r]) if slots is not None else -1
+        for j, (tb, te) in enumerate(sp):
+            head = [r, tb, te, j, L, p & 0xFFFFFFFF, (p >> 32) & 0xFFFFFFFF,
+                    s & 0xFFFFFFFF, (s >> 32) & 0xFFFFFFFF]
+            rec[b, :PLAN_PAGE0] = head
+            idx = np.minimum(tb // block_size + np.arange(PLAN_WORDS - PLAN_PAGE0),
+                             table.shape[1] - 1)
+            rec[b, PLAN_PAGE0:] = table[r, idx].astype(np.int64) & 0xFFFFFFFF
+            b += 1
+    assert b <= nrec
+    return rec

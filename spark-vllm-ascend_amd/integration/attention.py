@@ -14,10 +14,17 @@ vLLM's AttentionBackend / AttentionImpl method names:
       attn_metadata, output=None)
       writes key/value at slot_mapping, runs split-KV decode and the LSE
       merge (HIP kernels), returns [num_tokens, n_q * head_dim] bf16.
+  SplitKVDecodeBackend.plan(attn_metadata, block_size, num_heads, head_size)
+      once per step for a batch: cuts the live tokens into per-sequence
+      splits of one length (a device kernel), which every layer's forward
+      then uses (the reference's device-side task list, parts = ceil(length
+      / width): src/spark_vllm_ascend/kernels/attention.py:120-128).
 
 Metadata lives in device tensors (block tables, sequence lengths, slots) so
-a captured graph can replay with new values; only ``num_splits`` is fixed at
-capture time.
+a captured graph can replay with new values; only ``num_splits`` (and a
+plan's ``num_items``) is fixed at capture time.  The split partials are a
+workspace shared by every layer (layers run one after another on a stream):
+a plan clears the slots its splits do not write, once for all layers.
 """
 from __future__ import annotations
 
@@ -35,6 +42,8 @@ class SplitKVDecodeMetadata:
     slot_mapping: torch.Tensor    # int64 [num_tokens], -1 = skip
     num_splits: int
     max_seq_len: int = 0          # host hint used only to choose num_splits
+    num_items: int = 0            # a plan's split budget (SplitKVDecodeBackend.plan)
+    plan: torch.Tensor | None = None  # int32 [num_items + num_seqs, 64] plan records
 
 
 def choose_num_splits(capacity: int, tokens_per_split: int = 128, num_seqs: int = 1) -> int:
@@ -55,6 +64,33 @@ def choose_num_splits(capacity: int, tokens_per_split: int = 128, num_seqs: int 
     return min(n, 25) if num_seqs > 1 else n
 
 
+def choose_plan(num_seqs: int, n_kv: int = 8) -> tuple[int, int]:
+    """(num_items, num_splits) of a per-sequence split plan: one round of
+    three 4-wave workgroups per CU on a 256-CU part ((num_items + num_seqs)
+    * n_kv ~= 768), and at most 16 splits per sequence.  Measured on the
+    8-sequence step (contexts 512..32768, 115k tokens): 88 items / 16
+    splits 5.06 ms; 32 splits 5.14 ms (the merge reads num_seqs * num_splits
+    partial slots, the unused ones cleared); 56 / 120 / 184 items at 32
+    splits 5.13-5.15 / 5.19 / 5.19 ms; capacity splits 5.34 ms."""
+    return max(1, 768 // n_kv - num_seqs), 16
+
+
+_WORKSPACES: dict = {}
+
+
+def _workspace(num_seqs: int, num_splits: int, num_heads: int, head_size: int, device):
+    """Split partials, allocated once per shape and shared by every layer
+    (the reference likewise allocates its workspaces once per compile key,
+    src/spark_vllm_ascend/integration/model.py:128-131)."""
+    key = (num_seqs, num_splits, num_heads, head_size, torch.device(device))
+    if key not in _WORKSPACES:
+        _WORKSPACES[key] = (
+            torch.empty((num_seqs, num_splits, num_heads, head_size), dtype=torch.float32,
+                        device=device),
+            torch.empty((num_seqs, num_splits, num_heads), dtype=torch.float32, device=device))
+    return _WORKSPACES[key]
+
+
 class SplitKVDecodeImpl:
     def __init__(self, num_heads: int, head_size: int, scale: float, num_kv_heads: int,
                  **unused):
@@ -66,20 +102,6 @@ class SplitKVDecodeImpl:
         self.head_size = head_size
         self.scale = float(scale)
         self.num_kv_heads = num_kv_heads
-        self._workspaces = {}
-
-    def _workspace(self, num_seqs: int, num_splits: int, device):
-        """Split partials, allocated once per shape (the reference likewise
-        allocates its workspaces once per compile key,
-        src/spark_vllm_ascend/integration/model.py:128-131)."""
-        key = (num_seqs, num_splits, device)
-        if key not in self._workspaces:
-            self._workspaces[key] = (
-                torch.empty((num_seqs, num_splits, self.num_heads, self.head_size),
-                            dtype=torch.float32, device=device),
-                torch.empty((num_seqs, num_splits, self.num_heads), dtype=torch.float32,
-                            device=device))
-        return self._workspaces[key]
 
     def forward(self, layer, query: torch.Tensor, key: torch.Tensor | None,
                 value: torch.Tensor | None, kv_cache: torch.Tensor,
@@ -92,11 +114,18 @@ class SplitKVDecodeImpl:
                                         value.reshape(-1, self.num_kv_heads, self.head_size),
                                         k_cache, v_cache, attn_metadata.slot_mapping)
         q = query.reshape(num_seqs, self.num_heads, self.head_size)
-        po, pl = self._workspace(num_seqs, attn_metadata.num_splits, query.device)
+        po, pl = _workspace(num_seqs, attn_metadata.num_splits, self.num_heads, self.head_size,
+                            query.device)
         out = output.view(num_seqs, self.num_heads, self.head_size) if output is not None else None
-        out = torch_ops.splitkv_decode_merged(q, k_cache, v_cache, attn_metadata.block_tables,
-                                              attn_metadata.seq_lens, attn_metadata.num_splits,
-                                              self.scale, po, pl, out=out)
+        if attn_metadata.plan is not None:
+            out = torch_ops.splitkv_decode_planned_merged(
+                q, k_cache, v_cache, attn_metadata.block_tables, attn_metadata.plan,
+                attn_metadata.num_items, self.scale, po, pl, out=out)
+        else:
+            out = torch_ops.splitkv_decode_merged(q, k_cache, v_cache, attn_metadata.block_tables,
+                                                  attn_metadata.seq_lens,
+                                                  attn_metadata.num_splits, self.scale, po, pl,
+                                                  out=out)
         return out.view(num_seqs, self.num_heads * self.head_size)
 
 
@@ -112,6 +141,22 @@ class SplitKVDecodeBackend:
     @staticmethod
     def get_metadata_cls():
         return SplitKVDecodeMetadata
+
+    @staticmethod
+    def plan(attn_metadata: SplitKVDecodeMetadata, block_size: int, num_heads: int,
+             head_size: int) -> SplitKVDecodeMetadata:
+        """Per-sequence split plan for this step's metadata (num_items > 0,
+        at most 64 sequences), enqueued on the current stream; every layer's
+        forward with this metadata then runs over the plan's splits."""
+        if attn_metadata.num_items <= 0:
+            raise ValueError("set num_items (choose_plan) before planning")
+        num_seqs = attn_metadata.seq_lens.numel()
+        po, pl = _workspace(num_seqs, attn_metadata.num_splits, num_heads, head_size,
+                            attn_metadata.seq_lens.device)
+        attn_metadata.plan = torch_ops.splitkv_plan(
+            attn_metadata.seq_lens, attn_metadata.block_tables, block_size,
+            attn_metadata.num_items, po, pl, plan=attn_metadata.plan)
+        return attn_metadata
 
     @staticmethod
     def get_supported_head_sizes() -> list[int]:

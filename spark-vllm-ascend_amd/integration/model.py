@@ -40,7 +40,7 @@ from dataclasses import dataclass
 import torch
 
 from ..native import torch_ops
-from .attention import choose_num_splits
+from .attention import choose_num_splits, choose_plan
 from .head import TiedQ4_0Head
 from .linear import Q4_0Linear
 from .weights import synthetic_q4_0
@@ -110,11 +110,12 @@ class DecodeModel:
     `batch` sequences per step (one token each).  batch == 1 runs the fused
     GEMV path; batch > 1 runs the MFMA Q4_0 GEMM (m = batch rows) with
     separate add+RMSNorm launches and the fused q/k-norm + RoPE + KV-write
-    split-KV kernel, over a block table with one row per sequence."""
+    split-KV kernel over a per-sequence split plan (one plan launch per
+    step), over a block table with one row per sequence."""
 
     def __init__(self, cfg: DecoderConfig, device, seed: int = 0, max_len: int = 8192,
                  num_splits: int | None = None, weights: dict | None = None,
-                 fused: bool = True, batch: int = 1):
+                 fused: bool = True, batch: int = 1, plan_items: int | None = None):
         if not 1 <= batch <= 16:
             raise ValueError("batch must be in [1, 16]")
         self.cfg = cfg
@@ -160,8 +161,13 @@ class DecodeModel:
         self.head = TiedQ4_0Head(head_blocks.to(self.device), c.vocab, c.hidden)
         self.cos_sin = rope_cos_sin_cache(max_len, c.head_dim, c.rope_theta, self.device)
         self.scale = 1.0 / math.sqrt(c.head_dim)
-        self.num_splits = num_splits or choose_num_splits(blocks_per_seq * c.block_size,
-                                                          num_seqs=B)
+        if B == 1:
+            self.num_items = 0
+            self.num_splits = num_splits or choose_num_splits(blocks_per_seq * c.block_size)
+        else:
+            items, splits = choose_plan(B, c.n_kv)
+            self.num_items = plan_items or items
+            self.num_splits = num_splits or splits
 
         # pages are handed out in a seeded shuffled order, to exercise paging
         perm = torch.randperm(self.num_blocks, generator=torch.Generator().manual_seed(seed))
@@ -195,6 +201,8 @@ class DecodeModel:
         self.partial_o = torch.empty((B, self.num_splits, c.n_q, c.head_dim), dtype=torch.float32,
                                      device=dev)
         self.partial_lse = torch.empty((B, self.num_splits, c.n_q), dtype=torch.float32, device=dev)
+        self.plan = (torch.empty((self.num_items + B, torch_ops.PLAN_WORDS), dtype=torch.int32,
+                                 device=dev) if self.num_items else None)
         nk = torch_ops.argmax_keys_size(c.vocab, c.hidden) if B == 1 else 0
         self.argmax_keys = (torch.empty((1, nk), dtype=torch.int64, device=dev) if nk > 0
                             else None)
@@ -243,10 +251,10 @@ class DecodeModel:
             B = self.batch
             ops.add_rmsnorm(x_in, r_in, L.input_norm, c.eps, out=self.h, residual_out=self.res_a)
             ops.q4_0_gemm(self.h, L.qkv.qweight, c.qkv_rows, c.hidden, out=self.qkv_out)
-            ops.qknorm_rope_splitkv_decode_merged(
-                self.qkv_out, L.q_norm, L.k_norm, self.cos_sin, st.positions, st.slot_mapping,
-                L.kv_cache[0], L.kv_cache[1], st.block_table, st.seq_lens, self.num_splits,
-                self.scale, c.eps, c.n_q, self.partial_o, self.partial_lse, out=self.attn)
+            ops.qknorm_rope_splitkv_decode_planned_merged(
+                self.qkv_out, L.q_norm, L.k_norm, self.cos_sin, L.kv_cache[0], L.kv_cache[1],
+                st.block_table, self.plan, self.num_items, self.scale, c.eps, c.n_q,
+                self.partial_o, self.partial_lse, out=self.attn)
             ops.q4_0_gemm(self.attn.view(B, -1), L.o_proj.qweight, c.hidden, c.n_q * c.head_dim,
                           out=self.o)
             ops.add_rmsnorm(self.o, self.res_a, L.post_norm, c.eps, out=self.h2,
@@ -276,6 +284,12 @@ class DecodeModel:
         ops = torch_ops
         # self.x holds the embedding of st.ids: gathered by the previous
         # step's advance kernel, or by reset() / set_context()
+        if self.plan is not None:
+            # this step's splits from the lengths / positions / slots the
+            # previous advance left; every layer's attention reads them
+            ops.splitkv_plan(st.seq_lens, st.block_table, c.block_size, self.num_items,
+                             self.partial_o, self.partial_lse, positions=st.positions,
+                             slot_mapping=st.slot_mapping, plan=self.plan)
         for i in range(len(self.layers)):
             self.layer_run(i)
         x_in, r_in = self._layer_input(len(self.layers))

@@ -16,7 +16,7 @@ import ctypes
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libsmx.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 SMX_EINVAL = 10001
 SMX_EUNSUPPORTED = 10002
 
@@ -39,6 +39,12 @@ SIGNATURES = {
                                               _P, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32,
                                               _I32, _F32, _F32],
     "smx_lse_merge": [_P, _P, _P, _P, _I32, _I32, _I32, _I32],
+    "smx_splitkv_plan": [_P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _I32],
+    "smx_splitkv_decode_planned_merged": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32,
+                                          _I32, _I32, _I32, _I32, _I32, _I32, _F32],
+    "smx_qknorm_rope_splitkv_decode_planned_merged": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                                      _P, _I32, _I32, _I32, _I32, _I32, _I32,
+                                                      _I32, _I32, _I32, _I32, _F32, _F32],
     "smx_q4_0_gemm": [_P, _P, _P, _P, _I64, _I64, _I64],
     "smx_q4_0_gemm_swiglu": [_P, _P, _P, _P, _I64, _I64, _I64],
     "smx_compute_slot_mapping": [_P, _P, _I32, _P, _P, _P, _I32, _I32, _I32, _I32],

@@ -9,12 +9,16 @@
 // reported with lse = max + log(sum).
 //
 // Work decomposition (decode is HBM-bound: 512 bytes of K+V per token and kv
-// head against ~2k flops): one workgroup per (split, kv head, sequence) whose
-// waves stream 64-token blocks with all loads of a block in flight at once
-// (details at splitkv_decode_kernel), then a separate merge kernel.  The
-// merge is a second launch rather than a "last workgroup merges" epilogue:
-// on this multi-XCD part the device-scope fence that epilogue needs writes
-// back and invalidates each XCD's L2, which cost more than a launch.
+// head against ~2k flops): one workgroup per (kv head, split, sequence) whose
+// waves stream 32- or 64-token blocks with all loads of a block in flight at
+// once (details at splitkv_decode_kernel), then a separate merge kernel.
+// Splits are either cut from the block table's capacity (one sequence: the
+// first page lookups need no length) or taken from a per-step plan that cuts
+// the batch's live tokens into equal per-sequence splits
+// (splitkv_plan_kernel).  The merge is a second launch rather than a "last
+// workgroup merges" epilogue: on this multi-XCD part the device-scope fence
+// that epilogue needs writes back and invalidates each XCD's L2, which cost
+// more than a launch.
 #include <math.h>
 
 #include "smx_common.h"
@@ -29,19 +33,23 @@ constexpr int TILE = 32;   // tokens per wave iteration
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 
-// One workgroup of WAVES waves per (split, kv head, sequence).  Split s
-// covers [s*T, s*T + T) of the block table's capacity C (T = 32-aligned
-// ceil(C / num_splits)), clipped to the sequence length; its WAVES waves
-// take contiguous 32-aligned chunks and walk them in 64-token blocks.  Per block every K and V load is issued before
-// any arithmetic (128 VGPRs of data in flight per lane).
-//  QK: 8 lanes per token; lane c of a token owns the 16-byte chunks c and
-//      c + 8 of the 256-byte row, so each load instruction reads whole
-//      128-byte lines.  q (4 heads) is staged once per workgroup in LDS.
-//  softmax: after the 8-lane reduction every lane keeps the score of head
-//      lane & 3 only; maxima are reduced over the lanes sharing lane & 3.
-//  PV: 16 lanes per token, 8 dims each; two tokens' V are spliced into bf16
-//      pairs (v_perm_b32) that meet the bf16 probability pairs, staged in
-//      LDS, in v_dot2c_f32_bf16.
+// One workgroup of WAVES waves per (kv head, split, sequence).  Without a
+// plan, split s covers [s*T, s*T + T) of the block table's capacity C
+// (T = 32-aligned ceil(C / num_splits)), clipped to the sequence length; with
+// a plan, workgroup y takes the token range of plan record y.  The WAVES waves
+// take contiguous 32-aligned chunks of the split and walk them in BLK-token
+// blocks, every K and V load of a block issued before any arithmetic; QK^T
+// and PV run on v_mfma_f32_16x16x32_bf16 (operand layouts at load_block).
+//
+// Plan records (PLAN_WORDS uint32 words each, written by
+// splitkv_plan_kernel): word 0 the sequence (-1: unused record), 1 / 2 the
+// first / end token, 3 the split index within the sequence, 4 the sequence
+// length, 5-6 the position and 7-8 the slot (int64, little-endian), and
+// words PLAN_PAGE0..63 the block-table entries from the first token's page on.
+constexpr int PLAN_WORDS = 64;
+constexpr int PLAN_PAGE0 = 9;
+constexpr int PLAN_ALIGN = 128;  // split lengths are multiples of this (4 waves x 32 tokens)
+
 struct SplitKVArgs {
   const uint16_t* q;  // [num_seqs, n_q, HD] (plain) or the raw QKV row (FUSEQ)
   const uint16_t* kc;
@@ -84,13 +92,19 @@ __device__ __forceinline__ void norm_rope_head(float a, float b, float ga, float
 // first loads issue without a kernarg fetch.  pa_ / pb_ are the positions
 // and slots (FUSEQ: the per-sequence gather reads them at entry) or the K and
 // V caches (plain: read as soon as the first pages are known).
-template <int WAVES, int BLK, bool FUSEQ>
-__global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(
-    const int32_t* block_table_, const int32_t* seq_lens_, const void* pa_, const void* pb_,
+// lens_ is seq_lens, or with PLAN the plan records.
+// With a plan, at least two waves per SIMD (left to itself the compiler
+// gives the 4-wave 64-token variant 277 registers, one workgroup per CU);
+// without, the compiler's choice (the one-sequence step measured 1.7% slower
+// with the bound, which moves the MFMA accumulators out of AGPRs).
+template <int WAVES, int BLK, bool FUSEQ, bool PLAN>
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(PLAN ? 2 : 1)))
+void splitkv_decode_kernel(
+    const int32_t* block_table_, const void* lens_, const void* pa_, const void* pb_,
     const uint16_t* q_, int num_splits_, int max_blocks_, int bs_log2_, int n_kv_,
     SplitKVArgs A) {
   A.block_table = block_table_;
-  A.seq_lens = seq_lens_;
+  A.seq_lens = (const int32_t*)lens_;
   if constexpr (FUSEQ) {
     A.positions = (const int64_t*)pa_;
     A.slot_mapping = (const int64_t*)pb_;
@@ -120,52 +134,65 @@ __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(
   __shared__ float m_w[WAVES][G], l_w[WAVES][G];
   __shared__ int bad_w[WAVES];
 
-  // Dispatch order is kv head fastest, then split, then sequence: the
-  // workgroups of one kv head share an XCD (workgroups go to the 8 XCDs
+  // Dispatch order is kv head fastest, then split (or plan record), then
+  // sequence: the workgroups of one kv head share an XCD (workgroups go to the 8 XCDs
   // round-robin) and the 8 heads of the same tokens -- one 2 KB K row and
   // one V row per token -- are read together.  Measured: 2% off one
   // sequence's decode step against split-fastest; split-slowest made an
   // 8-sequence step 15% slower.
-  const int kvh = blockIdx.x, split = blockIdx.y, seq = blockIdx.z;
+  const int kvh = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  // Split and wave boundaries follow from the block table's capacity, not
-  // from the sequence length, so the first page lookups, the length and q
-  // are all loaded in one round trip.
   const int cap = max_blocks << bs_log2;
-  const int tps = ((cap + num_splits - 1) / num_splits + TILE - 1) / TILE * TILE;
-  const int wlen = ((tps + WAVES - 1) / WAVES + TILE - 1) / TILE * TILE;
-  const int s0 = split * tps;
-  const int w0 = min(s0 + wave * wlen, cap);
-  const int32_t* bt = block_table + (int64_t)seq * max_blocks;
-  // The wave-uniform values this workgroup starts from (length, the first
-  // two pages of the wave's chunk, position and slot) in ONE vector load,
-  // one address per lane, then v_readlane: scalar loads would each cost a
-  // full lgkmcnt(0) wait (their results return out of order), and the
-  // compiler issues them one by one next to their uses.
+  // The wave-uniform values this workgroup starts from come in ONE vector
+  // load, one address per lane, read back with v_readlane: scalar loads would
+  // each cost a full lgkmcnt(0) wait (their results return out of order), and
+  // the compiler issues them one by one next to their uses.
+  //  capacity splits: lane 0 the length, 3-4 the position, 5-6 the slot,
+  //    lanes 8..63 the pages of the wave's chunk from its first one on;
+  //  plan: the record (layout above).
+  // With capacity splits the bounds follow from the block table's capacity,
+  // not from the length, so all of it is one round trip; a plan record holds
+  // the bounds and the first pages itself.
+  constexpr int PB = PLAN ? PLAN_PAGE0 : 8;  // lane of the first gathered page
+  constexpr int LEN_LANE = PLAN ? 4 : 0, POS_LANE = PLAN ? 5 : 3, SLOT_LANE = PLAN ? 7 : 5;
   uint32_t gv;
-  {
+  int seq, split, s0, s_end, wlen, w0, pg0;
+  if constexpr (PLAN) {
+    gv = reinterpret_cast<const uint32_t*>(lens_)[(int64_t)blockIdx.y * PLAN_WORDS + lane];
+    seq = __builtin_amdgcn_readlane((int)gv, 0);
+    if (seq < 0) return;  // an unused record: the plan cleared the unused partials
+    s0 = __builtin_amdgcn_readlane((int)gv, 1);
+    s_end = __builtin_amdgcn_readlane((int)gv, 2);
+    split = __builtin_amdgcn_readlane((int)gv, 3);
+    wlen = ((s_end - s0 + WAVES - 1) / WAVES + TILE - 1) / TILE * TILE;
+    w0 = min(s0 + wave * wlen, s_end);
+    pg0 = s0 >> bs_log2;
+  } else {
+    split = blockIdx.y;
+    seq = blockIdx.z;
+    const int tps = ((cap + num_splits - 1) / num_splits + TILE - 1) / TILE * TILE;
+    wlen = ((tps + WAVES - 1) / WAVES + TILE - 1) / TILE * TILE;
+    s0 = split * tps;
+    s_end = s0 + tps;
+    w0 = min(s0 + wave * wlen, cap);
+    pg0 = w0 < cap ? (w0 >> bs_log2) : 0;
     const uint32_t* src = reinterpret_cast<const uint32_t*>(A.seq_lens + seq);
-    if (lane == 1) src = reinterpret_cast<const uint32_t*>(bt + (w0 < cap ? (w0 >> bs_log2) : 0));
-    if (lane == 2)
-      src = reinterpret_cast<const uint32_t*>(bt + (w0 + 32 < cap ? ((w0 + 32) >> bs_log2) : 0));
     if constexpr (FUSEQ) {
       if (lane == 3 || lane == 4)
         src = reinterpret_cast<const uint32_t*>(A.positions + seq) + (lane - 3);
       if (lane == 5 || lane == 6)
         src = reinterpret_cast<const uint32_t*>(A.slot_mapping + seq) + (lane - 5);
     }
-    // lanes 8..63: the pages of the wave's chunk from the first one on, so
-    // a wave that walks several blocks looks their pages up with v_readlane
-    // instead of a scalar-load round trip per block
-    if (lane >= 8) {
-      const int pg = (w0 < cap ? (w0 >> bs_log2) : 0) + (lane - 8);
-      src = reinterpret_cast<const uint32_t*>(bt + min(pg, max_blocks - 1));
-    }
+    if (lane >= 8)
+      src = reinterpret_cast<const uint32_t*>(block_table + (int64_t)seq * max_blocks +
+                                              min(pg0 + lane - 8, max_blocks - 1));
     gv = *src;
   }
+  const int32_t* bt = block_table + (int64_t)seq * max_blocks;
   // FUSEQ: this workgroup's q heads and the new token's k/v from the raw QKV
-  // row, issued in the same round trip (their addresses need nothing loaded).
+  // row; with capacity splits they are issued in the same round trip (their
+  // addresses need nothing loaded), with a plan right after the record.
   constexpr int HPW = (G + WAVES - 1) / WAVES;  // q heads per wave (FUSEQ)
   float qa[HPW], qb[HPW], qga = 0.f, qgb = 0.f, c = 0.f, sn = 0.f;
   float ka = 0.f, kb = 0.f, kga = 0.f, kgb = 0.f;
@@ -196,12 +223,21 @@ __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(
   auto lane_u32 = [&](int l) -> uint32_t {
     return (uint32_t)__builtin_amdgcn_readlane((int)gv, l);
   };
-  const int bt0 = (int)lane_u32(1);
-  const int bt1 = (int)lane_u32(2);
-  const int L = min((int)lane_u32(0), cap);
+  // page of token t >= the first gathered page: from the gather while it
+  // covers t, else a block-table load
+  auto page_of = [&](int t) -> int {
+    const int li = (t >> bs_log2) - pg0 + PB;
+    return li < 64 ? (int)lane_u32(li) : bt[min(t >> bs_log2, max_blocks - 1)];
+  };
+  // the first two pages: with capacity splits always gathered (lanes PB and
+  // PB or PB + 1: no branch), with a plan maybe past the record
+  const int bt0 = PLAN ? page_of(w0) : (int)lane_u32(PB);
+  const int bt1 = PLAN ? page_of(w0 + 32) : (int)lane_u32(PB + (((w0 + 32) >> bs_log2) - pg0));
+  const int L = min((int)lane_u32(LEN_LANE), cap);
   int64_t pos = 0;
-  if constexpr (FUSEQ) pos = (int64_t)(((uint64_t)lane_u32(4) << 32) | lane_u32(3));
-  const int s1 = min(L, s0 + tps);
+  if constexpr (FUSEQ)
+    pos = (int64_t)(((uint64_t)lane_u32(POS_LANE + 1) << 32) | lane_u32(POS_LANE));
+  const int s1 = min(L, s_end);
   float* po = part_o + (((int64_t)seq * num_splits + split) * n_q + kvh * G) * HD;
   float* pl = part_lse + ((int64_t)seq * num_splits + split) * n_q + kvh * G;
   // An empty split (no token below the length) leaves (0, -inf).  Its exit
@@ -249,13 +285,6 @@ __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(
   //    whole 256-byte rows per load.
   constexpr int NT16 = BLK / 16, NS32 = BLK / 32;
   u32x4 kr[NT16][4], vr[NS32][8];
-  // page of token t >= w0: gathered at entry for the first 56 pages of the
-  // chunk (lanes 8..63), else a block-table load
-  const int pg0 = w0 < cap ? (w0 >> bs_log2) : 0;
-  auto page_of = [&](int t) -> int {
-    const int li = (t >> bs_log2) - pg0 + 8;
-    return li < 64 ? (int)lane_u32(li) : bt[t >> bs_log2];
-  };
   auto load_block = [&](int t0) {
     const int64_t b0 = half_base(t0, t0 == w0 ? bt0 : page_of(t0));
     const int64_t b1 = BLK == 64 && t0 + 32 < w1
@@ -285,11 +314,11 @@ __global__ __launch_bounds__(64 * WAVES) void splitkv_decode_kernel(
   int64_t slot = -1;
   u32x4 qv = u32x4{0u, 0u, 0u, 0u};
   if constexpr (FUSEQ) {
-    owner = pos >= s0 && pos < s0 + tps && pos < L;
+    owner = pos >= s0 && pos < s1;
     const int64_t pc = pos < 0 ? 0 : (pos >= A.max_position ? A.max_position - 1 : pos);
     c = bf16_bits_to_f32(A.cos_sin[pc * HD + lane]);
     sn = bf16_bits_to_f32(A.cos_sin[pc * HD + 64 + lane]);
-    slot = (int64_t)(((uint64_t)lane_u32(6) << 32) | lane_u32(5));
+    slot = (int64_t)(((uint64_t)lane_u32(SLOT_LANE + 1) << 32) | lane_u32(SLOT_LANE));
   } else {
     qv = reinterpret_cast<const u32x4*>(A.q + ((int64_t)seq * n_q + kvh * G) * HD)[lane];
   }
@@ -581,15 +610,98 @@ __global__ __launch_bounds__(64 * MERGE_WAVES) void lse_merge_kernel(
   out[((int64_t)seq * n_q + h) * HD + d] = f32_to_bf16(r);
 }
 
+
+// Per-sequence split plan for a batch of decode sequences (the device-side
+// task list of execute_serial, src/spark_vllm_ascend/kernels/attention.py:
+// 120-128, where parts = ceil(length / width) follows the live length): the
+// batch's T = sum_r L_r live tokens are cut into splits of one length
+//   chunk = PLAN_ALIGN * ceil(max(ceil(T / num_items),
+//                                 ceil(max_r L_r / num_splits), 1) / PLAN_ALIGN)
+// that never cross a sequence, so sequence r has n_r = ceil(L_r / chunk) <=
+// num_splits splits and sum_r n_r <= num_items + num_seqs (the record count).
+// Items are numbered sequence by sequence; record b describes item b, or is
+// unused (sequence -1) past the last item.  Every workgroup reads all lengths
+// (one per lane, num_seqs <= 64) and derives the same plan; workgroup b
+// writes record b and clears partial slot b = (sequence, split) when no item
+// writes it (partial 0, lse -inf), so the merge over num_splits slots sees
+// empty splits there.  One launch serves every layer of a decode step.
+__device__ __forceinline__ int wave_sum_i32(int v) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+__device__ __forceinline__ int wave_max_i32(int v) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) v = max(v, __shfl_xor(v, o));
+  return v;
+}
+
+__global__ __launch_bounds__(64) void splitkv_plan_kernel(
+    const int32_t* __restrict__ seq_lens, const int64_t* __restrict__ positions,
+    const int64_t* __restrict__ slot_mapping, const int32_t* __restrict__ block_table,
+    uint32_t* __restrict__ plan, float* __restrict__ part_o, float* __restrict__ part_lse,
+    int num_seqs, int num_items, int num_splits, int max_blocks, int bs_log2, int n_q) {
+  const int lane = threadIdx.x;
+  const int b = blockIdx.x;
+  const int cap = max_blocks << bs_log2;
+  const int L = lane < num_seqs ? min(max(seq_lens[lane], 0), cap) : 0;
+  const int total = wave_sum_i32(L);  // <= num_seqs * cap < 2^31 (checked on the host)
+  const int lmax = wave_max_i32(L);
+  int chunk = max(max((total + num_items - 1) / num_items, (lmax + num_splits - 1) / num_splits), 1);
+  chunk = (chunk + PLAN_ALIGN - 1) / PLAN_ALIGN * PLAN_ALIGN;
+  const int n = (L + chunk - 1) / chunk;  // splits of this lane's sequence
+  int incl = n;                           // inclusive prefix sum over the lanes
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_up(incl, o);
+    if (lane >= o) incl += t;
+  }
+  const int n_items = __shfl(incl, 63);
+  if (b < num_items + num_seqs) {
+    uint32_t w = lane == 0 ? 0xffffffffu : 0u;  // unused record
+    if (b < n_items) {
+      // the sequence holding item b: the first lane whose prefix passes b
+      const int i = __ffsll((unsigned long long)__ballot(incl > b)) - 1;
+      const int li = __shfl(L, i);
+      const int j = b - (__shfl(incl, i) - __shfl(n, i));
+      const int tb = j * chunk, te = min(tb + chunk, li);
+      const int64_t p = positions ? positions[i] : 0;
+      const int64_t sl = slot_mapping ? slot_mapping[i] : -1;
+      const uint32_t head[PLAN_PAGE0] = {(uint32_t)i, (uint32_t)tb, (uint32_t)te, (uint32_t)j,
+                                         (uint32_t)li, (uint32_t)p, (uint32_t)(p >> 32),
+                                         (uint32_t)sl, (uint32_t)(sl >> 32)};
+      if (lane < PLAN_PAGE0) {
+#pragma unroll
+        for (int k = 0; k < PLAN_PAGE0; ++k)
+          if (lane == k) w = head[k];
+      } else {
+        w = (uint32_t)block_table[(int64_t)i * max_blocks +
+                                  min((tb >> bs_log2) + lane - PLAN_PAGE0, max_blocks - 1)];
+      }
+    }
+    plan[(int64_t)b * PLAN_WORDS + lane] = w;
+  }
+  if (b < num_seqs * num_splits) {
+    const int seq = b / num_splits;
+    if (b - seq * num_splits >= __shfl(n, seq)) {
+      f32x4* po = reinterpret_cast<f32x4*>(part_o + (int64_t)b * n_q * HD);
+      for (int e = lane; e < n_q * HD / 4; e += 64) po[e] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int h = lane; h < n_q; h += 64) part_lse[(int64_t)b * n_q + h] = -INFINITY;
+    }
+  }
+}
+
 }  // namespace
 }  // namespace smx
 
 #include "smx_abi_util.h"
 
 namespace {
+// plan: the plan records (num_records of them), or null for capacity splits.
 template <bool FUSEQ>
 int launch_splitkv(void* stream, smx::SplitKVArgs a, int32_t num_seqs, int32_t block_size,
-                   float scale) {
+                   float scale, const uint32_t* plan = nullptr, int num_records = 0) {
   int bs_log2 = 0;
   while ((1 << bs_log2) < block_size) ++bs_log2;
   a.bs_log2 = bs_log2;
@@ -600,6 +712,14 @@ int launch_splitkv(void* stream, smx::SplitKVArgs a, int32_t num_seqs, int32_t b
   const int64_t tps = ((cap + a.num_splits - 1) / a.num_splits + 31) / 32 * 32;
   int blk = tps <= 256 ? 32 : 64;
   int waves = blk == 64 ? 8 : tps <= 32 ? 1 : tps <= 64 ? 2 : tps <= 128 ? 4 : 8;
+  // A plan's splits are long (the batch's tokens over a few hundred
+  // workgroups): 4 waves of 32-token blocks, three workgroups per CU (168
+  // VGPRs; 64-token blocks take 246, two workgroups per CU, and measured
+  // 4% slower on an 8-sequence step).
+  if (plan) {
+    blk = 32;
+    waves = 4;
+  }
   const char* e = getenv("SMX_ATTN_WAVES");  // "waves[,blk]" override for tuning sweeps
   if (e) {
     int w = 0, b = 0;
@@ -607,13 +727,22 @@ int launch_splitkv(void* stream, smx::SplitKVArgs a, int32_t num_seqs, int32_t b
     if (n >= 1 && (w == 1 || w == 2 || w == 4 || w == 8)) waves = w;
     if (n == 2 && (b == 32 || b == 64)) blk = b;
   }
-  const dim3 grid(a.n_kv, a.num_splits, num_seqs);
+  const dim3 grid = plan ? dim3(a.n_kv, num_records, 1) : dim3(a.n_kv, a.num_splits, num_seqs);
 #define SMX_ATTN_LAUNCH(W, B)                                                                   \
-  hipLaunchKernelGGL((smx::splitkv_decode_kernel<W, B, FUSEQ>), grid, dim3(64 * W), 0,          \
-                     (hipStream_t)stream, a.block_table, a.seq_lens,                               \
-                     FUSEQ ? (const void*)a.positions : (const void*)a.kc,                         \
-                     FUSEQ ? (const void*)a.slot_mapping : (const void*)a.vc, a.q, a.num_splits,   \
-                     a.max_blocks, a.bs_log2, a.n_kv, a)
+  do {                                                                                          \
+    if (plan)                                                                                   \
+      hipLaunchKernelGGL((smx::splitkv_decode_kernel<W, B, FUSEQ, true>), grid, dim3(64 * W),   \
+                         0, (hipStream_t)stream, a.block_table, (const void*)plan,                \
+                         FUSEQ ? (const void*)a.positions : (const void*)a.kc,                     \
+                         FUSEQ ? (const void*)a.slot_mapping : (const void*)a.vc, a.q,             \
+                         a.num_splits, a.max_blocks, a.bs_log2, a.n_kv, a);                        \
+    else                                                                                        \
+      hipLaunchKernelGGL((smx::splitkv_decode_kernel<W, B, FUSEQ, false>), grid, dim3(64 * W),  \
+                         0, (hipStream_t)stream, a.block_table, (const void*)a.seq_lens,          \
+                         FUSEQ ? (const void*)a.positions : (const void*)a.kc,                     \
+                         FUSEQ ? (const void*)a.slot_mapping : (const void*)a.vc, a.q,             \
+                         a.num_splits, a.max_blocks, a.bs_log2, a.n_kv, a);                        \
+  } while (0)
   if (blk == 32) {
     if (waves == 8) SMX_ATTN_LAUNCH(8, 32);
     else if (waves == 4) SMX_ATTN_LAUNCH(4, 32);
@@ -753,5 +882,91 @@ extern "C" int smx_lse_merge(void* stream, const float* partial_o, const float* 
   SMX_REQUIRE((uintptr_t)out % 2 == 0 && (uintptr_t)partial_o % 4 == 0 &&
                   (uintptr_t)partial_lse % 4 == 0,
               "misaligned pointer");
+  return launch_merge(stream, partial_o, partial_lse, out, num_seqs, num_splits, n_q);
+}
+
+#define SMX_PLAN_CHECKS()                                                                        \
+  SMX_REQUIRE(plan, "null plan");                                                                \
+  SMX_REQUIRE(num_seqs <= 64, "a plan covers at most 64 sequences");                             \
+  SMX_REQUIRE(num_items >= 1 && num_items + num_seqs <= 65535,                                   \
+              "num_items must be >= 1 with num_items + num_seqs <= 65535");                      \
+  SMX_REQUIRE((uintptr_t)plan % 4 == 0, "plan must be 4-byte aligned")
+
+extern "C" int smx_splitkv_plan(void* stream, const int32_t* seq_lens, const int64_t* positions,
+                                const int64_t* slot_mapping, const int32_t* block_table,
+                                uint32_t* plan, float* partial_o, float* partial_lse,
+                                int32_t num_seqs, int32_t num_items, int32_t num_splits,
+                                int32_t max_blocks, int32_t block_size, int32_t n_q,
+                                int32_t head_dim) {
+  SMX_REQUIRE(seq_lens && block_table && partial_o && partial_lse, "null pointer argument");
+  SMX_REQUIRE(num_seqs >= 1, "num_seqs must be >= 1");
+  SMX_PLAN_CHECKS();
+  SMX_REQUIRE(num_splits >= 1 && num_splits <= 4096, "num_splits must be in [1, 4096]");
+  SMX_REQUIRE(max_blocks >= 1, "max_blocks must be >= 1");
+  SMX_REQUIRE(block_size >= 32 && block_size <= 4096 && (block_size & (block_size - 1)) == 0,
+              "block_size must be a power of two in [32, 4096]");
+  SMX_REQUIRE((int64_t)num_seqs * max_blocks * block_size <= INT32_MAX,
+              "num_seqs * max_blocks * block_size must fit in int32");
+  SMX_REQUIRE(head_dim == 128 && n_q >= 1 && n_q <= 65535, "head_dim must be 128");
+  SMX_REQUIRE((uintptr_t)seq_lens % 4 == 0 && (uintptr_t)block_table % 4 == 0 &&
+                  (uintptr_t)positions % 8 == 0 && (uintptr_t)slot_mapping % 8 == 0 &&
+                  (uintptr_t)partial_o % 16 == 0 && (uintptr_t)partial_lse % 4 == 0,
+              "misaligned pointer (partial_o needs 16 bytes)");
+  int bs_log2 = 0;
+  while ((1 << bs_log2) < block_size) ++bs_log2;
+  const int64_t grid = std::max<int64_t>(num_items + num_seqs, (int64_t)num_seqs * num_splits);
+  hipLaunchKernelGGL(smx::splitkv_plan_kernel, dim3((unsigned)grid), dim3(64), 0,
+                     (hipStream_t)stream, seq_lens, positions, slot_mapping, block_table, plan,
+                     partial_o, partial_lse, num_seqs, num_items, num_splits, max_blocks, bs_log2,
+                     n_q);
+  return (int)hipGetLastError();
+}
+
+extern "C" int smx_splitkv_decode_planned_merged(
+    void* stream, const void* q, const void* k_cache, const void* v_cache,
+    const int32_t* block_table, const uint32_t* plan, float* partial_o, float* partial_lse,
+    void* out, int32_t num_seqs, int32_t num_items, int32_t num_splits, int32_t max_blocks,
+    int32_t num_blocks, int32_t block_size, int32_t n_q, int32_t n_kv, int32_t head_dim,
+    float scale) {
+  const void* seq_lens = plan;  // the plan's records carry the lengths
+  SMX_SPLITKV_CHECKS();
+  SMX_PLAN_CHECKS();
+  SMX_REQUIRE(out && (uintptr_t)out % 2 == 0, "out must be non-null and 2-byte aligned");
+  const int rc = launch_splitkv<false>(
+      stream,
+      splitkv_args(q, k_cache, v_cache, block_table, nullptr, partial_o, partial_lse, num_splits,
+                   max_blocks, num_blocks, n_q, n_kv),
+      num_seqs, block_size, scale, plan, num_items + num_seqs);
+  if (rc) return rc;
+  return launch_merge(stream, partial_o, partial_lse, out, num_seqs, num_splits, n_q);
+}
+
+extern "C" int smx_qknorm_rope_splitkv_decode_planned_merged(
+    void* stream, const void* qkv, const void* q_gamma, const void* k_gamma,
+    const void* cos_sin, void* k_cache, void* v_cache, const int32_t* block_table,
+    const uint32_t* plan, float* partial_o, float* partial_lse, void* out, int32_t num_seqs,
+    int32_t num_items, int32_t num_splits, int32_t max_blocks, int32_t num_blocks,
+    int32_t block_size, int32_t n_q, int32_t n_kv, int32_t head_dim, int32_t max_position,
+    float eps, float scale) {
+  const void* q = qkv;
+  const void* seq_lens = plan;  // the plan's records carry lengths, positions and slots
+  SMX_SPLITKV_CHECKS();
+  SMX_PLAN_CHECKS();
+  SMX_REQUIRE(q_gamma && k_gamma && cos_sin && out, "null pointer argument");
+  SMX_REQUIRE(max_position >= 1, "max_position must be >= 1");
+  SMX_REQUIRE(eps >= 0.f && isfinite(eps), "eps must be finite and >= 0");
+  SMX_REQUIRE((uintptr_t)out % 2 == 0 && (uintptr_t)q_gamma % 2 == 0 &&
+                  (uintptr_t)k_gamma % 2 == 0 && (uintptr_t)cos_sin % 2 == 0,
+              "misaligned pointer");
+  smx::SplitKVArgs a = splitkv_args(qkv, k_cache, v_cache, block_table, nullptr, partial_o,
+                                    partial_lse, num_splits, max_blocks, num_blocks, n_q, n_kv);
+  a.q_gamma = (const uint16_t*)q_gamma;
+  a.k_gamma = (const uint16_t*)k_gamma;
+  a.cos_sin = (const uint16_t*)cos_sin;
+  a.max_position = max_position;
+  a.eps = eps;
+  const int rc = launch_splitkv<true>(stream, a, num_seqs, block_size, scale, plan,
+                                      num_items + num_seqs);
+  if (rc) return rc;
   return launch_merge(stream, partial_o, partial_lse, out, num_seqs, num_splits, n_q);
 }

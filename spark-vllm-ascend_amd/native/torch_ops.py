@@ -148,6 +148,72 @@ def lse_merge(partial_o: torch.Tensor, partial_lse: torch.Tensor,
     return out
 
 
+PLAN_WORDS = 64  # uint32 words per split-plan record (SMX_SPLITKV_PLAN_WORDS)
+
+
+def splitkv_plan(seq_lens: torch.Tensor, block_table: torch.Tensor, block_size: int,
+                 num_items: int, partial_o: torch.Tensor, partial_lse: torch.Tensor,
+                 positions: torch.Tensor | None = None, slot_mapping: torch.Tensor | None = None,
+                 plan: torch.Tensor | None = None) -> torch.Tensor:
+    """Per-sequence split plan from the live lengths (device-side; one call
+    per decode step serves every layer).  partial_o [seqs, num_splits, n_q,
+    hd] / partial_lse fix num_splits and must be the buffers the planned
+    attention calls use: slots no split writes are cleared here.  Returns
+    the plan, int32 [num_items + seqs, PLAN_WORDS] (uint32 words)."""
+    num_seqs = seq_lens.numel()
+    _need(partial_o.dim() == 4 and partial_o.shape[0] == num_seqs,
+          "partial_o must be [seqs, splits, n_q, hd]")
+    _, num_splits, n_q, hd = partial_o.shape
+    _check(seq_lens, "seq_lens", torch.int32, num_seqs)
+    _check(block_table, "block_table", torch.int32, device=seq_lens.device)
+    _need(block_table.dim() == 2 and block_table.shape[0] == num_seqs, "block_table must be [seqs, max_blocks]")
+    _check(partial_o, "partial_o", torch.float32, device=seq_lens.device)
+    _check(partial_lse, "partial_lse", torch.float32, num_seqs * num_splits * n_q, seq_lens.device)
+    for t, name in ((positions, "positions"), (slot_mapping, "slot_mapping")):
+        if t is not None:
+            _check(t, name, torch.int64, num_seqs, seq_lens.device)
+    nrec = num_items + num_seqs
+    if plan is None:
+        plan = torch.empty((nrec, PLAN_WORDS), dtype=torch.int32, device=seq_lens.device)
+    _check(plan, "plan", torch.int32, nrec * PLAN_WORDS, seq_lens.device)
+    call("smx_splitkv_plan", _stream(seq_lens), seq_lens.data_ptr(), _ptr(positions),
+         _ptr(slot_mapping), block_table.data_ptr(), plan.data_ptr(), partial_o.data_ptr(),
+         partial_lse.data_ptr(), num_seqs, num_items, num_splits, block_table.shape[1],
+         block_size, n_q, hd)
+    return plan
+
+
+def splitkv_decode_planned_merged(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                                  block_table: torch.Tensor, plan: torch.Tensor, num_items: int,
+                                  scale: float, partial_o: torch.Tensor, partial_lse: torch.Tensor,
+                                  out: torch.Tensor | None = None) -> torch.Tensor:
+    """splitkv_decode_merged over the splits of a plan (splitkv_plan with the
+    same block table, num_items and partial buffers)."""
+    _need(q.dim() == 3 and k_cache.dim() == 4, "q must be [seqs, n_q, hd], caches 4-D")
+    num_seqs, n_q, hd = q.shape
+    num_blocks, bs, n_kv, hd2 = k_cache.shape
+    _need(hd == hd2, "head_dim mismatch between q and the cache")
+    _need(tuple(v_cache.shape) == tuple(k_cache.shape), "k_cache and v_cache shapes differ")
+    _check(q, "q", BF16)
+    _check(k_cache, "k_cache", BF16, device=q.device)
+    _check(v_cache, "v_cache", BF16, device=q.device)
+    _check(block_table, "block_table", torch.int32, device=q.device)
+    _need(block_table.dim() == 2 and block_table.shape[0] == num_seqs, "block_table must be [seqs, max_blocks]")
+    _check(plan, "plan", torch.int32, (num_items + num_seqs) * PLAN_WORDS, q.device)
+    _need(partial_o.dim() == 4 and partial_o.shape[0] == num_seqs, "partial_o must be [seqs, splits, n_q, hd]")
+    num_splits = partial_o.shape[1]
+    _check(partial_o, "partial_o", torch.float32, num_seqs * num_splits * n_q * hd, q.device)
+    _check(partial_lse, "partial_lse", torch.float32, num_seqs * num_splits * n_q, q.device)
+    if out is None:
+        out = torch.empty((num_seqs, n_q, hd), dtype=BF16, device=q.device)
+    _check(out, "out", BF16, num_seqs * n_q * hd, q.device)
+    call("smx_splitkv_decode_planned_merged", _stream(q), q.data_ptr(), k_cache.data_ptr(),
+         v_cache.data_ptr(), block_table.data_ptr(), plan.data_ptr(), partial_o.data_ptr(),
+         partial_lse.data_ptr(), out.data_ptr(), num_seqs, num_items, num_splits,
+         block_table.shape[1], num_blocks, bs, n_q, n_kv, hd, float(scale))
+    return out
+
+
 def add_rmsnorm(x: torch.Tensor, residual: torch.Tensor | None, gamma: torch.Tensor, eps: float,
                 out: torch.Tensor | None = None, residual_out: torch.Tensor | None = None):
     """Returns (y, residual_out).  With residual=None: y = RMSNorm(x), residual_out = x."""
@@ -403,6 +469,44 @@ def qknorm_rope_splitkv_decode_merged(qkv: torch.Tensor, q_gamma: torch.Tensor,
          k_gamma.data_ptr(), cos_sin.data_ptr(), positions.data_ptr(), slot_mapping.data_ptr(),
          k_cache.data_ptr(), v_cache.data_ptr(), block_table.data_ptr(), seq_lens.data_ptr(),
          partial_o.data_ptr(), partial_lse.data_ptr(), out.data_ptr(), num_seqs, num_splits,
+         block_table.shape[1], num_blocks, bs, n_q, n_kv, hd, cos_sin.shape[0], float(eps),
+         float(scale))
+    return out
+
+
+def qknorm_rope_splitkv_decode_planned_merged(qkv: torch.Tensor, q_gamma: torch.Tensor,
+                                              k_gamma: torch.Tensor, cos_sin: torch.Tensor,
+                                              k_cache: torch.Tensor, v_cache: torch.Tensor,
+                                              block_table: torch.Tensor, plan: torch.Tensor,
+                                              num_items: int, scale: float, eps: float, n_q: int,
+                                              partial_o: torch.Tensor, partial_lse: torch.Tensor,
+                                              out: torch.Tensor | None = None) -> torch.Tensor:
+    """qknorm_rope_splitkv_decode_merged over the splits of a plan; the
+    positions and slots come from the plan (splitkv_plan given them)."""
+    num_blocks, bs, n_kv, hd = k_cache.shape
+    num_seqs = block_table.shape[0]
+    _check(qkv, "qkv", BF16, num_seqs * (n_q + 2 * n_kv) * hd)
+    _check(q_gamma, "q_gamma", BF16, hd, qkv.device)
+    _check(k_gamma, "k_gamma", BF16, hd, qkv.device)
+    _check(cos_sin, "cos_sin", BF16, device=qkv.device)
+    _need(cos_sin.dim() == 2 and cos_sin.shape[1] == hd, "cos_sin must be [max_position, head_dim]")
+    _check(k_cache, "k_cache", BF16, device=qkv.device)
+    _check(v_cache, "v_cache", BF16, device=qkv.device)
+    _need(tuple(v_cache.shape) == tuple(k_cache.shape), "k_cache and v_cache shapes differ")
+    _check(block_table, "block_table", torch.int32, device=qkv.device)
+    _need(block_table.dim() == 2, "block_table must be [seqs, max_blocks]")
+    _check(plan, "plan", torch.int32, (num_items + num_seqs) * PLAN_WORDS, qkv.device)
+    _need(partial_o.dim() == 4 and partial_o.shape[0] == num_seqs, "partial_o must be [seqs, splits, n_q, hd]")
+    num_splits = partial_o.shape[1]
+    _check(partial_o, "partial_o", torch.float32, num_seqs * num_splits * n_q * hd, qkv.device)
+    _check(partial_lse, "partial_lse", torch.float32, num_seqs * num_splits * n_q, qkv.device)
+    if out is None:
+        out = torch.empty((num_seqs, n_q, hd), dtype=BF16, device=qkv.device)
+    _check(out, "out", BF16, num_seqs * n_q * hd, qkv.device)
+    call("smx_qknorm_rope_splitkv_decode_planned_merged", _stream(qkv), qkv.data_ptr(),
+         q_gamma.data_ptr(), k_gamma.data_ptr(), cos_sin.data_ptr(), k_cache.data_ptr(),
+         v_cache.data_ptr(), block_table.data_ptr(), plan.data_ptr(), partial_o.data_ptr(),
+         partial_lse.data_ptr(), out.data_ptr(), num_seqs, num_items, num_splits,
          block_table.shape[1], num_blocks, bs, n_q, n_kv, hd, cos_sin.shape[0], float(eps),
          float(scale))
     return out

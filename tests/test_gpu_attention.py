@@ -9,7 +9,7 @@ import pytest
 from oracle import attention as oatt
 from oracle.bf16 import bf16_bits_to_f32
 
-from _util import bf16_dev, f32_of, pkg, randn_bf16
+from _util import bf16_dev, bits_of, f32_of, pkg, randn_bf16
 
 pytestmark = pytest.mark.gpu
 
@@ -206,3 +206,131 @@ def test_zero_length_gives_zero_output(ops, dev, merged):
     q, kc, vc, table = _case(rng, [1, 1], 128)
     out, _, pl = _run(ops, dev, q, kc, vc, table, [0, 0], 8, HD ** -0.5, merged=merged)
     assert np.all(out == 0)
+
+
+def _planned(ops, dev, q, kc, vc, table, lengths, bs, items, splits, scale,
+             positions=None, slots=None):
+    """Plan + planned decode over partial buffers that start as NaN (slots
+    no split writes must be cleared by the plan)."""
+    import torch
+    ns = len(lengths)
+    po = torch.full((ns, splits, N_Q, HD), float("nan"), dtype=torch.float32, device=dev)
+    pl = torch.full((ns, splits, N_Q), float("nan"), dtype=torch.float32, device=dev)
+    tdev = torch.from_numpy(table).to(dev)
+    t64 = lambda a: None if a is None else torch.tensor(a, dtype=torch.int64, device=dev)
+    plan = ops.splitkv_plan(torch.tensor(lengths, dtype=torch.int32, device=dev), tdev, bs, items,
+                            po, pl, positions=t64(positions), slot_mapping=t64(slots))
+    out = ops.splitkv_decode_planned_merged(bf16_dev(q, dev), bf16_dev(kc, dev), bf16_dev(vc, dev),
+                                            tdev, plan, items, scale, po, pl)
+    return f32_of(out), po.cpu().numpy(), pl.cpu().numpy(), plan.cpu().numpy()
+
+
+@pytest.mark.parametrize("lengths,bs,items,splits", [
+    ([31075 // 8, 12494 // 8, 6639 // 8, 1, 0, 2000], 128, 24, 16),
+    ([300], 32, 56, 8), ([0, 0], 128, 8, 4), ([5000, 17], 64, 3, 2)])
+def test_plan_records_match_oracle(ops, dev, lengths, bs, items, splits):
+    rng = np.random.default_rng(len(lengths) * 7 + items)
+    q, kc, vc, table = _case(rng, [max(L, 1) for L in lengths], bs)
+    pos = [L - 1 for L in lengths]
+    slots = [int(rng.integers(-1, 1 << 20)) for _ in lengths]
+    _, _, _, plan = _planned(ops, dev, q, kc, vc, table, lengths, bs, items, splits,
+                             HD ** -0.5, positions=pos, slots=slots)
+    ref = oatt.plan_records(lengths, items, splits, table, bs, positions=pos, slots=slots)
+    np.testing.assert_array_equal(plan.view(np.uint32), ref)
+
+
+@pytest.mark.parametrize("lengths,bs,items,splits", [
+    ([512, 3000, 77, 8192, 1, 0, 129], 128, 24, 16),
+    ([512, 3000, 77, 8192, 1, 0, 129], 32, 56, 64),
+    ([6144], 128, 49, 64), ([20000], 32, 1, 1), ([9000, 40], 128, 2, 2)])
+def test_planned_vs_fp64(ops, dev, lengths, bs, items, splits):
+    """Merged outputs against float64 attention, every split's partial against
+    the oracle's online softmax over the plan's bounds, and the slots no
+    split writes cleared to (0, -inf).  ([20000] with 32-token pages and one
+    split: the waves' pages beyond the record's 55 come from the table.)"""
+    rng = np.random.default_rng(sum(lengths) + items)
+    q, kc, vc, table = _case(rng, [max(L, 1) for L in lengths], bs)
+    scale = HD ** -0.5
+    out, po, pl, _ = _planned(ops, dev, q, kc, vc, table, lengths, bs, items, splits, scale)
+    qf, kf, vf = (bf16_bits_to_f32(a) for a in (q, kc, vc))
+    out = out.reshape(len(lengths), N_Q, HD)
+    _, sp = oatt.plan_splits(lengths, items, splits, table.shape[1] * bs)
+    for i, L in enumerate(lengths):
+        if L == 0:
+            assert np.all(out[i] == 0)
+        else:
+            k = oatt.gather_paged(kf, table[i], L)
+            v = oatt.gather_paged(vf, table[i], L)
+            ref = oatt.attention_f64(qf[i], k, v, scale)
+            assert np.max(np.abs(out[i] - ref)) < 2e-2, f"sequence {i} (L={L})"
+            opo, opl = oatt.splitkv_partials(qf[i], k, v, scale, sp[i])
+            n = len(sp[i])
+            assert np.max(np.abs(pl[i, :n] - opl)) < 1e-3
+            assert np.max(np.abs(po[i, :n] - opo)) < 2e-2
+        n = len(sp[i])
+        assert np.all(po[i, n:] == 0) and np.all(pl[i, n:] == -np.inf), f"sequence {i} unused slots"
+
+
+def test_planned_page_permutation_invariance(ops, dev):
+    rng = np.random.default_rng(18)
+    lengths, bs = [1500, 700], 128
+    q, kc, vc, table = _case(rng, lengths, bs, extra_blocks=0)
+    perm = rng.permutation(kc.shape[0])
+    inv = np.argsort(perm)
+    table2 = table.copy()
+    for i, L in enumerate(lengths):
+        nb = -(-L // bs)
+        table2[i, :nb] = inv[table[i, :nb]]
+    a = _planned(ops, dev, q, kc, vc, table, lengths, bs, 5, 8, HD ** -0.5)[0]
+    b = _planned(ops, dev, q, kc[perm], vc[perm], table2, lengths, bs, 5, 8, HD ** -0.5)[0]
+    np.testing.assert_array_equal(a, b)
+
+
+def test_plan_rejects_bad_shapes(ops, dev):
+    import torch
+    SmxError = pkg("native").SmxError
+    sl = torch.ones(65, dtype=torch.int32, device=dev)
+    table = torch.zeros((65, 2), dtype=torch.int32, device=dev)
+    po = torch.empty((65, 4, N_Q, HD), dtype=torch.float32, device=dev)
+    pl = torch.empty((65, 4, N_Q), dtype=torch.float32, device=dev)
+    with pytest.raises(SmxError, match="at most 64"):
+        ops.splitkv_plan(sl, table, 128, 8, po, pl)
+
+
+@pytest.mark.parametrize("planned", [False, True])
+def test_backend_forward(dev, planned):
+    """The vLLM-style backend: forward writes key/value at the slots and
+    returns the merged attention, with capacity splits or with a plan built
+    once for the step and shared by two layers' calls."""
+    import torch
+    att = pkg("integration.attention")
+    rng = np.random.default_rng(21 + planned)
+    lengths, bs = [700, 3000, 1], 128
+    q, kc, vc, table = _case(rng, lengths, bs)
+    backend = att.SplitKVDecodeBackend
+    impl = backend.get_impl_cls()(N_Q, HD, HD ** -0.5, N_KV)
+    kv = torch.stack([bf16_dev(kc, dev), bf16_dev(vc, dev)]).view(2, *kc.shape)
+    slots = [int(table[i, (L - 1) // bs]) * bs + (L - 1) % bs for i, L in enumerate(lengths)]
+    knew = randn_bf16(rng, (len(lengths), N_KV * HD))
+    vnew = randn_bf16(rng, (len(lengths), N_KV * HD))
+    items, splits = att.choose_plan(len(lengths), N_KV) if planned else (0, 8)
+    md = att.SplitKVDecodeMetadata(
+        block_tables=torch.from_numpy(table).to(dev),
+        seq_lens=torch.tensor(lengths, dtype=torch.int32, device=dev),
+        slot_mapping=torch.tensor(slots, dtype=torch.int64, device=dev), num_splits=splits,
+        num_items=items)
+    if planned:
+        backend.plan(md, bs, N_Q, HD)
+    outs = [impl.forward(None, bf16_dev(q, dev).view(len(lengths), -1), bf16_dev(knew, dev),
+                         bf16_dev(vnew, dev), kv, md) for _ in range(2)]
+    np.testing.assert_array_equal(f32_of(outs[0]), f32_of(outs[1]))
+    kf = bf16_bits_to_f32(bits_of(kv[0]).reshape(kc.shape))
+    vf = bf16_bits_to_f32(bits_of(kv[1]).reshape(vc.shape))
+    qf = bf16_bits_to_f32(q)
+    got = f32_of(outs[0]).reshape(len(lengths), N_Q, HD)
+    for i, L in enumerate(lengths):
+        blk, off = divmod(slots[i], bs)
+        np.testing.assert_array_equal(bits_of(kv[0][blk, off]).reshape(-1), knew[i])
+        ref = oatt.attention_f64(qf[i], oatt.gather_paged(kf, table[i], L),
+                                 oatt.gather_paged(vf, table[i], L), HD ** -0.5)
+        assert np.max(np.abs(got[i] - ref)) < 2e-2, f"sequence {i}"

@@ -232,3 +232,44 @@ def test_fused_uses_new_kv_over_stale_slot(ops, dev):
                      what="stale slot")
     assert bf16_ulp_diff(bits_of(kc1), bits_of(kc2)).max() <= 1
     np.testing.assert_array_equal(bits_of(vc1), bits_of(vc2))
+
+
+def _fused_planned(ops, c, items, splits, kc, vc):
+    import torch
+    ns = c["sl"].numel()
+    bs = kc.shape[1]
+    po = torch.full((ns, splits, N_Q, HD), float("nan"), dtype=torch.float32, device=kc.device)
+    pl = torch.full((ns, splits, N_Q), float("nan"), dtype=torch.float32, device=kc.device)
+    plan = ops.splitkv_plan(c["sl"], c["table"], bs, items, po, pl, positions=c["pos"],
+                            slot_mapping=c["slots"])
+    return ops.qknorm_rope_splitkv_decode_planned_merged(c["qkv"], c["qg"], c["kg"], c["cs"], kc, vc,
+                                                         c["table"], plan, items, HD ** -0.5, EPS,
+                                                         N_Q, po, pl)
+
+
+@pytest.mark.parametrize("lengths,bs,items,splits", [
+    ([1], 128, 8, 4), ([6144], 128, 49, 64), ([33, 129, 4096], 128, 8, 8),
+    ([97, 1000, 5000, 2], 32, 24, 16), ([512, 3000, 77, 2049, 1, 700, 6000, 129], 128, 56, 16)])
+def test_fused_planned(ops, dev, lengths, bs, items, splits):
+    """The planned fused kernel: the same cache writes as the two-launch path
+    and the float64 result over the updated cache, for ragged batches."""
+    rng = np.random.default_rng(sum(lengths) + items)
+    c = _fused_case(rng, lengths, bs, dev)
+    kc1, vc1 = c["kc"].clone(), c["vc"].clone()
+    kc2, vc2 = c["kc"].clone(), c["vc"].clone()
+    out = _fused_planned(ops, c, items, splits, kc1, vc1)
+    out2, q = _two_launch(ops, c, 8, kc2, vc2)
+    assert bf16_ulp_diff(bits_of(kc1), bits_of(kc2)).max() <= 1
+    np.testing.assert_array_equal(bits_of(vc1), bits_of(vc2))
+    ns = len(lengths)
+    assert_close_rel(f32_of(out).reshape(ns, -1), f32_of(out2).reshape(ns, -1), rtol=1e-2,
+                     atol_frac=1e-2, what="planned fused vs two-launch")
+    kcn = bf16_bits_to_f32(bits_of(kc1))
+    vcn = bf16_bits_to_f32(bits_of(vc1))
+    qf = f32_of(q).reshape(ns, N_Q, HD)
+    for i, L in enumerate(lengths):
+        k = oatt.gather_paged(kcn, c["np"]["table"][i], L)
+        v = oatt.gather_paged(vcn, c["np"]["table"][i], L)
+        ref = oatt.attention_f64(qf[i], k, v, HD ** -0.5)
+        got = f32_of(out).reshape(ns, N_Q, HD)[i]
+        assert np.abs(got - ref).max() < 2e-2, f"seq {i} (L={L})"

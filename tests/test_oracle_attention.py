@@ -92,3 +92,51 @@ def test_lse_of_single_split_is_logsumexp():
         s = (k[:, h // 4, :].astype(np.float64) @ q[h].astype(np.float64)) * 0.3
         lse = np.log(np.sum(np.exp(s - s.max()))) + s.max()
         assert abs(pl[0, h] - lse) < 1e-4
+
+
+PLAN_CASES = [([31075, 12494, 6639, 12989, 6118, 15990, 11664, 18505], 56, 16, 32896),
+              ([1], 56, 16, 128), ([0, 0, 0], 8, 4, 1024), ([512, 3000, 77, 8192, 1, 0], 24, 32, 8320),
+              ([40000, 10], 8, 4, 32768), ([5, 6, 7], 1, 1, 256), ([4096] * 64, 200, 8, 4096)]
+
+
+@pytest.mark.parametrize("lengths,items,splits,cap", PLAN_CASES)
+def test_plan_splits_tile_and_bounds(lengths, items, splits, cap):
+    chunk, sp = oatt.plan_splits(lengths, items, splits, cap)
+    L = [min(max(x, 0), cap) for x in lengths]
+    for l, s in zip(L, sp):
+        assert [t for a, e in s for t in range(a, e)] == list(range(l))
+        assert all(a % oatt.PLAN_ALIGN == 0 and e - a <= chunk for a, e in s)
+        assert len(s) <= splits
+    assert sum(len(s) for s in sp) <= items + len(lengths)
+    # chunk is the smallest multiple of 128 meeting both bounds (brute force)
+    ok = lambda c: c * items >= sum(L) and c * splits >= max(L) and c >= 1
+    assert ok(chunk) and chunk % 128 == 0
+    assert not any(ok(c) for c in range(128, chunk, 128))
+
+
+def test_plan_records_layout():
+    table = np.arange(3 * 70, dtype=np.int32).reshape(3, 70)
+    rec = oatt.plan_records([300, 0, 8000], 4, 8, table, 128, positions=[299, -1, 7999],
+                            slots=[5, -1, 1 << 33])
+    # chunk = 128 * ceil(max(ceil(8300 / 4), ceil(8000 / 8)) / 128) = 2176
+    assert rec.shape == (7, oatt.PLAN_WORDS)
+    assert rec[0, :5].tolist() == [0, 0, 300, 0, 300]
+    assert rec[0, 5:9].tolist() == [299, 0, 5, 0]
+    assert rec[0, 9:12].tolist() == [0, 1, 2]
+    assert rec[1, :5].tolist() == [2, 0, 2176, 0, 8000]
+    assert rec[1, 7:9].tolist() == [0, 2]                  # slot 2^33
+    assert rec[4, :5].tolist() == [2, 6528, 8000, 3, 8000]
+    assert rec[4, 9] == 140 + 6528 // 128                   # page of token 6528
+    assert rec[4, -1] == 140 + 69                           # clamped to the row's end
+    assert rec[5, 0] == 0xFFFFFFFF and not rec[5, 1:].any()  # unused
+
+
+@pytest.mark.parametrize("lengths,items,splits", [([700, 33, 1], 6, 4), ([2000, 500], 3, 8)])
+def test_planned_partials_merge_to_unsplit(lengths, items, splits):
+    rng = np.random.default_rng(sum(lengths))
+    _, sp = oatt.plan_splits(lengths, items, splits, 4096)
+    for L, bounds in zip(lengths, sp):
+        q, k, v = rand_case(rng, L)
+        ref = oatt.attention_f64(q, k, v, 128 ** -0.5)
+        po, pl = oatt.splitkv_partials(q, k, v, 128 ** -0.5, bounds)
+        assert np.max(np.abs(oatt.lse_merge(po, pl) - ref)) < 1e-2
