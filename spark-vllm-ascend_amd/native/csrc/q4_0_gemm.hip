@@ -186,11 +186,18 @@ __device__ __forceinline__ void transpose_rows4(uint32_t& r0, uint32_t& r1, uint
   r3 = d[1];
 }
 
-template <bool SWIGLU>
+// WS > 0 (m <= 2 WS <= 8): a wave copies its tile's activations -- m rows x
+// 512 bytes, WS 16-byte loads per lane -- into a private LDS slice and reads
+// the MFMA A operands from there (8 loads per tile straight from global
+// memory cost 8 vector-memory instructions per tile whatever m is).  Chunk
+// c of row r sits at 16 (r * 32 + (c ^ (r & 7))) bytes of the slice, so the
+// rows of one operand read fall in different banks.
+template <bool SWIGLU, int WS>
 __global__ __launch_bounds__(1024) void q4_0_gemm_tile_kernel(
     const uint8_t* w_, const uint16_t* x_, int npairs, int n_out, int64_t up_offset_rows, int ks,
     int m, int64_t ldx, uint16_t* y, int64_t ldy) {
   __shared__ f32x4 red[16][64];
+  extern __shared__ u32x4 xsl[];  // WS > 0: [ks][8 rows x 32 chunks]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n = lane & 15, j = lane >> 4;  // j is also the lane's k-group after the transpose
   int wrow;
@@ -220,10 +227,39 @@ __global__ __launch_bounds__(1024) void q4_0_gemm_tile_kernel(
     const uint32_t p8 = pw[8];
     // the activations of the tile's 8 blocks for this lane's row and k-group
     u32x4 xa[8];
+    if constexpr (WS > 0) {
+      u32x4* sl = xsl + wave * 256;
+      u32x4 sv[WS];
 #pragma unroll
-    for (int b = 0; b < 8; ++b) {
-      const int pp = min(4 * t + (b >> 1), npairs - 1);
-      xa[b] = *reinterpret_cast<const u32x4*>(xr + pp * 64 + (b & 1) * 32 + 8 * j);
+      for (int i = 0; i < WS; ++i) {  // chunk c: row c >> 5, pair (c & 31) >> 3, 8 elements c & 7
+        const int c = i * 64 + lane;
+        const int pp = min(4 * t + ((c & 31) >> 3), npairs - 1);
+        sv[i] = *reinterpret_cast<const u32x4*>(x_ + (int64_t)min(c >> 5, m - 1) * ldx + pp * 64 +
+                                                (c & 7) * 8);
+      }
+#pragma unroll
+      for (int i = 0; i < WS; ++i) {
+        const int c = i * 64 + lane, r = c >> 5;
+        sl[r * 32 + ((c & 31) ^ (r & 7))] = sv[i];
+      }
+      // the slice is private to this wave: its LDS operations complete in
+      // order, so only the compiler has to be kept from reordering
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const int xrow = min(n, m - 1);
+#pragma unroll
+      for (int b = 0; b < 8; ++b)
+        xa[b] = sl[xrow * 32 + ((((b >> 1) * 8 + (b & 1) * 4 + j)) ^ (xrow & 7))];
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    } else {
+#pragma unroll
+      for (int b = 0; b < 8; ++b) {
+        const int pp = min(4 * t + (b >> 1), npairs - 1);
+        xa[b] = *reinterpret_cast<const u32x4*>(xr + pp * 64 + (b & 1) * 32 + 8 * j);
+      }
     }
     // qs dwords of the even block (bytes 2..17 of the pair) and the odd one
     // (bytes 20..35), and the two scales packed (d_even | d_odd << 16)
@@ -294,9 +330,18 @@ hipError_t launch_gemm_tile(hipStream_t s, const void* x, const void* w, void* y
   const int ntiles = (npairs + 3) / 4;
   const int ks = ntiles < 16 ? ntiles : 16;
   const int grid = SWIGLU ? (int)((n_out + 7) / 8) : (int)((n_out + 15) / 16);
-  hipLaunchKernelGGL(q4_0_gemm_tile_kernel<SWIGLU>, dim3(grid), dim3(64 * ks), 0, s,
-                     (const uint8_t*)w, (const uint16_t*)x, npairs, (int)n_out, up_offset_rows, ks,
-                     (int)m, k, (uint16_t*)y, n_out);
+  int ws = m <= 2 ? 1 : m <= 4 ? 2 : m <= 8 ? 4 : 0;
+  if (const char* e = getenv("SMX_GEMM_WS")) ws = atoi(e) ? ws : 0;  // tuning sweeps
+  const size_t lds = ws ? (size_t)ks * 256 * 16 : 0;
+#define SMX_GEMM_LAUNCH(W)                                                                      \
+  hipLaunchKernelGGL((q4_0_gemm_tile_kernel<SWIGLU, W>), dim3(grid), dim3(64 * ks), lds, s,       \
+                     (const uint8_t*)w, (const uint16_t*)x, npairs, (int)n_out, up_offset_rows,   \
+                     ks, (int)m, k, (uint16_t*)y, n_out)
+  if (ws == 1) SMX_GEMM_LAUNCH(1);
+  else if (ws == 2) SMX_GEMM_LAUNCH(2);
+  else if (ws == 4) SMX_GEMM_LAUNCH(4);
+  else SMX_GEMM_LAUNCH(0);
+#undef SMX_GEMM_LAUNCH
   return hipGetLastError();
 }
 }  // namespace
