@@ -222,12 +222,18 @@ def batch_decode(dev, steps: int = 64, warmup: int = 4, batch: int = 8, seed: in
         + rb(c.vocab, c.hidden)
     mid = ctx.to(torch.float64) + warmup + steps / 2
     kv = int((mid * 2 * c.n_kv * c.head_dim * 2 * c.n_layers).sum())
+    model_items, model_splits = model.num_items, model.num_splits
     del model
     torch.cuda.empty_cache()
     return {"batch": batch, "contexts": ctx.tolist(), "steps": steps, "ms_per_step": round(dt * 1e3, 4),
-            "tok_s": round(batch / dt, 2), "bytes_per_step": weights + kv,
+            "tok_s": round(batch / dt, 2),
+            # every sequence advances one token per step: its TPOT is the step time
+            "tpot_ms_per_sequence": [round(dt * 1e3, 4)] * batch,
+            "plan": {"num_items": model_items, "num_splits": model_splits},
+            "bytes_per_step": weights + kv,
             "achieved_gbs": round((weights + kv) / dt / 1e9, 1),
-            "note": "8 sequences, contexts ~U[512, 32768] (seeded), random KV contents, greedy"}
+            "note": "8 sequences, contexts ~U[512, 32768] (seeded), random KV contents, greedy; "
+                    "split-KV over a per-sequence split plan"}
 
 
 def step_bytes(cfg, ctx: int) -> int:
