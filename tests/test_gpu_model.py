@@ -12,6 +12,7 @@
 import numpy as np
 import pytest
 
+from oracle import attention as oatt
 from oracle import model as omodel
 from oracle import ops as oops
 from oracle.bf16 import bf16_bits_to_f32
@@ -225,3 +226,33 @@ def test_batched_graph_replay_and_ragged_prompts(dev):
     for r, p in enumerate(prompts):
         np.testing.assert_array_equal(eager[r, :p.numel()], p.numpy())
     assert (eager[:, :16] >= 0).all() and (eager[:, :16] < 1000).all()
+
+
+def test_batched_plan_splits_change_under_graph_replay(dev):
+    """Through the captured graph, each step's plan re-cuts the splits from
+    the grown lengths: with 8 plan items a sequence has 1 split up to 128
+    tokens, then 2, then 3 (three sequences, 280 steps).  Every row's logits
+    match its own oracle decoder (checked every 7th step and at the end)."""
+    import torch
+    m = _m()
+    batch, T = 3, 280
+    model = m.DecodeModel(tiny_cfg(), dev, seed=11, max_len=320, batch=batch, plan_items=8,
+                          num_splits=4)
+    oracles = [oracle_from(model, num_splits=3) for _ in range(batch)]
+    rng = np.random.default_rng(11)
+    seqs = rng.integers(0, model.cfg.vocab, (batch, T))
+    model.capture()
+    model.reset([torch.from_numpy(s) for s in seqs])
+    splits_seen = set()
+    for pos in range(T):
+        model.step()
+        ols = [oracles[r].step(int(seqs[r, pos]), pos) for r in range(batch)]
+        if pos % 7 == 6 or pos == T - 1:
+            torch.cuda.synchronize()
+            gl = f32_of(model.logits).reshape(batch, -1)
+            for r in range(batch):
+                assert_close_rel(gl[r], ols[r], rtol=2e-2, atol_frac=2e-2, what=f"row {r} step {pos}")
+        cap = model.state.block_table.shape[1] * model.cfg.block_size
+        _, sp = oatt.plan_splits([pos + 1] * batch, 8, 4, cap)
+        splits_seen.add(len(sp[0]))
+    assert {1, 2, 3} <= splits_seen
