@@ -25,45 +25,51 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 
 // s = x + r (fp32); residual_out = bf16(s); y = bf16(s * inv_rms * gamma).
 // Follows norm_ub (src/spark_vllm_ascend/kernels/linear.py:202-224): the
-// normalised value uses the fp32 sum, not its bf16 rounding.  Each thread
-// owns 8-element chunks and writes only the indices it read, so
-// residual_out may alias residual.
-__global__ __launch_bounds__(256) void add_rmsnorm_kernel(
+// normalised value uses the fp32 sum, not its bf16 rounding.  One workgroup
+// per row, sized to the row (one or two 8-element chunks per thread): x, the
+// residual and gamma are all loaded up front, unconditionally from clamped
+// indices, so the row costs one round trip before the reduction (loads under
+// a branch, or gamma loaded after the reduction, each cost another).  Each
+// thread writes only the indices it read, so residual_out may alias residual.
+template <int CH, bool RES>
+__global__ __launch_bounds__(1024) void add_rmsnorm_kernel(
     const uint16_t* __restrict__ x, const uint16_t* residual, const uint16_t* __restrict__ gamma,
     uint16_t* __restrict__ y, uint16_t* residual_out, int hidden, float eps) {
   __shared__ float red[16];
   const int64_t row = blockIdx.x;
   const u32x4* xr = reinterpret_cast<const u32x4*>(x + row * hidden);
-  const u32x4* rr = residual ? reinterpret_cast<const u32x4*>(residual + row * hidden) : nullptr;
+  const u32x4* rr = reinterpret_cast<const u32x4*>((RES ? residual : x) + row * hidden);
+  const u32x4* gr = reinterpret_cast<const u32x4*>(gamma);
   const int nch = hidden / 8;
-  constexpr int MAXC = 8;  // hidden <= 8 * 256 * MAXC
-  float sv[MAXC][8];
+  u32x4 xa[CH], ra[CH], ga[CH];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int ch = min((int)threadIdx.x + c * (int)blockDim.x, nch - 1);
+    xa[c] = xr[ch];
+    if constexpr (RES) ra[c] = rr[ch];
+    ga[c] = gr[ch];
+  }
+  float sv[CH][8];
   float ss = 0.f;
 #pragma unroll
-  for (int c = 0; c < MAXC; ++c) {
-    const int ch = threadIdx.x + c * 256;
-    if (ch < nch) {
-      const u32x4 a = xr[ch];
-      const u32x4 b = rr ? rr[ch] : u32x4{0u, 0u, 0u, 0u};
-      const uint32_t aw[4] = {a.x, a.y, a.z, a.w};
-      const uint32_t bw[4] = {b.x, b.y, b.z, b.w};
+  for (int c = 0; c < CH; ++c) {
+    const bool ok = (int)threadIdx.x + c * (int)blockDim.x < nch;
+    const uint32_t aw[4] = {xa[c].x, xa[c].y, xa[c].z, xa[c].w};
+    const uint32_t bw[4] = {ra[c].x, ra[c].y, ra[c].z, ra[c].w};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        sv[c][2 * i] = bf16_lo(aw[i]) + bf16_lo(bw[i]);
-        sv[c][2 * i + 1] = bf16_hi(aw[i]) + bf16_hi(bw[i]);
-        ss += sv[c][2 * i] * sv[c][2 * i] + sv[c][2 * i + 1] * sv[c][2 * i + 1];
-      }
+    for (int i = 0; i < 4; ++i) {
+      sv[c][2 * i] = bf16_lo(aw[i]) + (RES ? bf16_lo(bw[i]) : 0.f);
+      sv[c][2 * i + 1] = bf16_hi(aw[i]) + (RES ? bf16_hi(bw[i]) : 0.f);
+      if (ok) ss += sv[c][2 * i] * sv[c][2 * i] + sv[c][2 * i + 1] * sv[c][2 * i + 1];
     }
   }
   ss = block_sum(ss, red);
   const float inv = 1.0f / sqrtf(ss / (float)hidden + eps);
-  const u32x4* gr = reinterpret_cast<const u32x4*>(gamma);
 #pragma unroll
-  for (int c = 0; c < MAXC; ++c) {
-    const int ch = threadIdx.x + c * 256;
+  for (int c = 0; c < CH; ++c) {
+    const int ch = (int)threadIdx.x + c * (int)blockDim.x;
     if (ch < nch) {
-      const u32x4 g = gr[ch];
-      const uint32_t gw[4] = {g.x, g.y, g.z, g.w};
+      const uint32_t gw[4] = {ga[c].x, ga[c].y, ga[c].z, ga[c].w};
       uint32_t yo[4], ro[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -379,10 +385,16 @@ extern "C" int smx_add_rmsnorm(void* stream, const void* x, const void* residual
   SMX_REQUIRE((uintptr_t)x % 16 == 0 && (uintptr_t)gamma % 16 == 0 && (uintptr_t)y % 16 == 0 &&
                   (uintptr_t)residual % 16 == 0 && (uintptr_t)residual_out % 16 == 0,
               "bf16 tensors must be 16-byte aligned");
-  hipLaunchKernelGGL(smx::add_rmsnorm_kernel, dim3((unsigned)rows), dim3(256), 0,
-                     (hipStream_t)stream, (const uint16_t*)x, (const uint16_t*)residual,
-                     (const uint16_t*)gamma, (uint16_t*)y, (uint16_t*)residual_out, (int)hidden,
-                     eps);
+  // one 8-element chunk per thread up to 1024 chunks (hidden 8192), else two
+  const int nch = (int)(hidden / 8);
+  const int threads = nch <= 1024 ? (nch + 63) / 64 * 64 : 1024;
+  const auto kern = nch <= 1024 ? (residual ? smx::add_rmsnorm_kernel<1, true>
+                                            : smx::add_rmsnorm_kernel<1, false>)
+                                : (residual ? smx::add_rmsnorm_kernel<2, true>
+                                            : smx::add_rmsnorm_kernel<2, false>);
+  hipLaunchKernelGGL(kern, dim3((unsigned)rows), dim3(threads), 0, (hipStream_t)stream,
+                     (const uint16_t*)x, (const uint16_t*)residual, (const uint16_t*)gamma,
+                     (uint16_t*)y, (uint16_t*)residual_out, (int)hidden, eps);
   return (int)hipGetLastError();
 }
 
