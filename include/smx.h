@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define SMX_ABI_VERSION 3
+#define SMX_ABI_VERSION 4
 
 /* Return codes besides 0 and hipError_t values. */
 #define SMX_EINVAL 10001      /* an argument failed validation */
@@ -354,6 +354,19 @@ int smx_q4_0_gemm(void* stream, const void* x, const void* w, void* y, int64_t m
  */
 int smx_q4_0_gemm_swiglu(void* stream, const void* x, const void* w, void* out, int64_t m,
                          int64_t d, int64_t k);
+
+/*
+ * smx_q4_0_gemm (x 16-byte aligned) that also writes greedy-argmax keys:
+ * keys[r][b] (b < smx_q4_0_gemm_keys_per_row(n) = ceil(n / 16)) is the
+ * largest (order-preserving bf16 key of y[r][o]) << 32 | (0xffffffff - o)
+ * over the outputs o of 16-column group b, for smx_decode_advance's
+ * argmax_keys (NaN largest, lowest index on ties).  The batched form of the
+ * head GEMV + greedy sampling (src/spark_vllm_ascend/integration/
+ * head.py:12-16 and the stock argmax), without a separate argmax launch.
+ */
+int64_t smx_q4_0_gemm_keys_per_row(int64_t n);
+int smx_q4_0_gemm_argmax(void* stream, const void* x, const void* w, void* y, uint64_t* keys,
+                         int64_t m, int64_t n, int64_t k);
 
 /*
  * Paged KV write (vLLM reshape_and_cache): for each token t with

@@ -203,8 +203,10 @@ class DecodeModel:
         self.partial_lse = torch.empty((B, self.num_splits, c.n_q), dtype=torch.float32, device=dev)
         self.plan = (torch.empty((self.num_items + B, torch_ops.PLAN_WORDS), dtype=torch.int32,
                                  device=dev) if self.num_items else None)
-        nk = torch_ops.argmax_keys_size(c.vocab, c.hidden) if B == 1 else 0
-        self.argmax_keys = (torch.empty((1, nk), dtype=torch.int64, device=dev) if nk > 0
+        # greedy-argmax keys: the head GEMV's (one row) or the head GEMM's
+        nk = (torch_ops.argmax_keys_size(c.vocab, c.hidden) if B == 1
+              else torch_ops.gemm_keys_per_row(c.vocab))
+        self.argmax_keys = (torch.empty((B, nk), dtype=torch.int64, device=dev) if nk > 0
                             else None)
         self.graph: torch.cuda.CUDAGraph | None = None
 
@@ -299,10 +301,11 @@ class DecodeModel:
                                         c.vocab, c.hidden, c.eps, self.argmax_keys.view(-1),
                                         out=self.logits)
             keys = self.argmax_keys
-        elif self.batch > 1:
+        elif self.batch > 1 and self.argmax_keys is not None:
             ops.add_rmsnorm(x_in, r_in, self.final_norm, c.eps, out=self.h)
-            ops.q4_0_gemm(self.h, self.head.q4_0_head, c.vocab, c.hidden, out=self.logits)
-            ops.argmax(self.logits, out=st.next_ids)
+            ops.q4_0_gemm_argmax(self.h, self.head.q4_0_head, c.vocab, c.hidden,
+                                 self.argmax_keys, out=self.logits)
+            keys = self.argmax_keys
         else:
             ops.add_rmsnorm(x_in, r_in, self.final_norm, c.eps, out=self.h)
             ops.q4_0_gemv(self.h, self.head.q4_0_head, c.vocab, c.hidden, out=self.logits)

@@ -16,7 +16,7 @@ import ctypes
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libsmx.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 SMX_EINVAL = 10001
 SMX_EUNSUPPORTED = 10002
 
@@ -47,6 +47,8 @@ SIGNATURES = {
                                                       _I32, _I32, _I32, _I32, _F32, _F32],
     "smx_q4_0_gemm": [_P, _P, _P, _P, _I64, _I64, _I64],
     "smx_q4_0_gemm_swiglu": [_P, _P, _P, _P, _I64, _I64, _I64],
+    "smx_q4_0_gemm_argmax": [_P, _P, _P, _P, _P, _I64, _I64, _I64],
+    "smx_q4_0_gemm_keys_per_row": [_I64],
     "smx_compute_slot_mapping": [_P, _P, _I32, _P, _P, _P, _I32, _I32, _I32, _I32],
     "smx_add_rmsnorm": [_P, _P, _P, _P, _P, _P, _I64, _I64, _F32],
     "smx_qknorm_rope_kv_write": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32,
@@ -64,7 +66,8 @@ SIGNATURES = {
 }
 
 # return types other than int
-RESTYPES = {"smx_q4_0_argmax_keys_size": ctypes.c_int64}
+RESTYPES = {"smx_q4_0_argmax_keys_size": ctypes.c_int64,
+            "smx_q4_0_gemm_keys_per_row": ctypes.c_int64}
 
 _lib = None
 

@@ -192,10 +192,13 @@ __device__ __forceinline__ void transpose_rows4(uint32_t& r0, uint32_t& r1, uint
 // memory cost 8 vector-memory instructions per tile whatever m is).  Chunk
 // c of row r sits at 16 (r * 32 + (c ^ (r & 7))) bytes of the slice, so the
 // rows of one operand read fall in different banks.
-template <bool SWIGLU, int WS>
+// KEYS (plain outputs): besides y, keys[row][blockIdx.x] is the greedy-argmax
+// key of the workgroup's 16 outputs of each row (bf16_order_key), which the
+// step-advance kernel reduces; the separate argmax launch is not needed.
+template <bool SWIGLU, int WS, bool KEYS = false>
 __global__ __launch_bounds__(1024) void q4_0_gemm_tile_kernel(
     const uint8_t* w_, const uint16_t* x_, int npairs, int n_out, int64_t up_offset_rows, int ks,
-    int m, int64_t ldx, uint16_t* y, int64_t ldy) {
+    int m, int64_t ldx, uint16_t* y, int64_t ldy, uint64_t* keys) {
   __shared__ f32x4 red[16][64];
   extern __shared__ u32x4 xsl[];  // WS > 0: [ks][8 rows x 32 chunks]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -320,12 +323,29 @@ __global__ __launch_bounds__(1024) void q4_0_gemm_tile_kernel(
         if (o < n_out) y[(int64_t)mr * ldy + o] = f32_to_bf16(total(nn));
       }
     }
+    if constexpr (KEYS && !SWIGLU) {
+      // the 16 outputs of row mr sit in lanes 16 q .. 16 q + 15 of this wave
+      const int o = blockIdx.x * 16 + nn;
+      uint64_t key = 0;
+      if (mr < m && o < n_out)
+        key = ((uint64_t)bf16_order_key(f32_to_bf16(total(nn))) << 32) |
+              (uint64_t)(0xffffffffu - (uint32_t)o);
+#pragma unroll
+      for (int s = 1; s < 16; s <<= 1) {
+        const uint64_t other =
+            ((uint64_t)(uint32_t)__shfl_xor((int)(key >> 32), s, 64) << 32) |
+            (uint32_t)__shfl_xor((int)(uint32_t)key, s, 64);
+        key = other > key ? other : key;
+      }
+      if (nn == 0 && mr < m) keys[(int64_t)mr * gridDim.x + blockIdx.x] = key;
+    }
   }
 }
 
-template <bool SWIGLU>
+template <bool SWIGLU, bool KEYS = false>
 hipError_t launch_gemm_tile(hipStream_t s, const void* x, const void* w, void* y, int64_t m,
-                            int64_t n_out, int64_t k, int64_t up_offset_rows) {
+                            int64_t n_out, int64_t k, int64_t up_offset_rows,
+                            uint64_t* keys = nullptr) {
   const int npairs = (int)(k / 64);
   const int ntiles = (npairs + 3) / 4;
   const int ks = ntiles < 16 ? ntiles : 16;
@@ -334,9 +354,9 @@ hipError_t launch_gemm_tile(hipStream_t s, const void* x, const void* w, void* y
   if (const char* e = getenv("SMX_GEMM_WS")) ws = atoi(e) ? ws : 0;  // tuning sweeps
   const size_t lds = ws ? (size_t)ks * 256 * 16 : 0;
 #define SMX_GEMM_LAUNCH(W)                                                                      \
-  hipLaunchKernelGGL((q4_0_gemm_tile_kernel<SWIGLU, W>), dim3(grid), dim3(64 * ks), lds, s,       \
-                     (const uint8_t*)w, (const uint16_t*)x, npairs, (int)n_out, up_offset_rows,   \
-                     ks, (int)m, k, (uint16_t*)y, n_out)
+  hipLaunchKernelGGL((q4_0_gemm_tile_kernel<SWIGLU, W, KEYS>), dim3(grid), dim3(64 * ks), lds,  \
+                     s, (const uint8_t*)w, (const uint16_t*)x, npairs, (int)n_out,                \
+                     up_offset_rows, ks, (int)m, k, (uint16_t*)y, n_out, keys)
   if (ws == 1) SMX_GEMM_LAUNCH(1);
   else if (ws == 2) SMX_GEMM_LAUNCH(2);
   else if (ws == 4) SMX_GEMM_LAUNCH(4);
@@ -380,4 +400,14 @@ extern "C" int smx_q4_0_gemm_swiglu(void* stream, const void* x, const void* w, 
   hipLaunchKernelGGL(smx::q4_0_gemm_kernel<true>, dim3((unsigned)((d + 7) / 8)), dim3(512), 0,
                      (hipStream_t)stream, a);
   return (int)hipGetLastError();
+}
+
+extern "C" int64_t smx_q4_0_gemm_keys_per_row(int64_t n) { return (n + 15) / 16; }
+
+extern "C" int smx_q4_0_gemm_argmax(void* stream, const void* x, const void* w, void* y,
+                                    uint64_t* keys, int64_t m, int64_t n, int64_t k) {
+  SMX_GEMM_CHECKS(n);
+  SMX_REQUIRE(keys && (uintptr_t)keys % 8 == 0, "keys must be non-null and 8-byte aligned");
+  SMX_REQUIRE((uintptr_t)x % 16 == 0, "x must be 16-byte aligned");
+  return (int)smx::launch_gemm_tile<false, true>((hipStream_t)stream, x, w, y, m, n, k, 0, keys);
 }

@@ -91,12 +91,6 @@ __device__ __forceinline__ float pair_dot(const Pair& w, const u32x4* xs, float 
   return acc;
 }
 
-// Order-preserving 16-bit key of a bf16 value (NaN above +inf).
-__device__ __forceinline__ uint32_t bf16_order_key(uint16_t b) {
-  if ((b & 0x7f80u) == 0x7f80u && (b & 0x7fu)) return 0xffffu;  // NaN
-  return (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
-}
-
 enum { EPI_STORE = 0, EPI_SWIGLU = 1, EPI_ARGMAX = 2 };
 
 struct GemvArgs {

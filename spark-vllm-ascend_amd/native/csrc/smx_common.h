@@ -38,6 +38,14 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t h16) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)h16);
 }
 
+// Order-preserving 16-bit key of a bf16 value (NaN above +inf).  Greedy
+// argmax keys are (key << 32) | (0xffffffff - index): the largest key is the
+// largest value, the lowest index among equal values.
+__device__ __forceinline__ uint32_t bf16_order_key(uint16_t b) {
+  if ((b & 0x7f80u) == 0x7f80u && (b & 0x7fu)) return 0xffffu;  // NaN
+  return (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
+}
+
 // acc + a.lo*b.lo + a.hi*b.hi, both operands packed bf16 pairs (v_dot2c_f32_bf16).
 __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float acc) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a),

@@ -564,3 +564,27 @@ def q4_0_gemm_swiglu(x: torch.Tensor, w: torch.Tensor, d: int, k: int,
     call("smx_q4_0_gemm_swiglu", _stream(x), x.data_ptr(), w.data_ptr(), out.data_ptr(),
          x.shape[0], d, k)
     return out
+
+
+def gemm_keys_per_row(n: int) -> int:
+    """Greedy-argmax keys q4_0_gemm_argmax writes per row (one per 16 outputs)."""
+    from . import load
+    return int(load().smx_q4_0_gemm_keys_per_row(n))
+
+
+def q4_0_gemm_argmax(x: torch.Tensor, w: torch.Tensor, n: int, k: int, keys: torch.Tensor,
+                     out: torch.Tensor | None = None) -> torch.Tensor:
+    """y = x W^T (m <= 16 rows) plus keys [m, ceil(n / 16)] int64 (uint64
+    bits), the greedy-argmax keys decode_advance(argmax_keys=keys) reduces."""
+    _need(x.dim() == 2 and x.shape[1] == k and 1 <= x.shape[0] <= 16, "x must be [m <= 16, k]")
+    m = x.shape[0]
+    _check(x, "x", BF16)
+    _need(x.data_ptr() % 16 == 0, "x must be 16-byte aligned")
+    _check(w, "w", torch.uint8, n * q4_0_row_bytes(k), x.device)
+    _check(keys, "keys", torch.int64, m * gemm_keys_per_row(n), x.device)
+    if out is None:
+        out = torch.empty((m, n), dtype=BF16, device=x.device)
+    _check(out, "out", BF16, m * n, x.device)
+    call("smx_q4_0_gemm_argmax", _stream(x), x.data_ptr(), w.data_ptr(), out.data_ptr(),
+         keys.data_ptr(), m, n, k)
+    return out

@@ -125,3 +125,33 @@ def test_gemm_rejects_bad_arguments(ops, dev):
         ops.q4_0_gemm(torch.zeros((17, 256), dtype=torch.bfloat16, device=dev), w, 64, 256)
     with pytest.raises(ValueError):
         ops.q4_0_gemm(torch.zeros((2, 256), dtype=torch.float32, device=dev), w, 64, 256)
+
+
+@pytest.mark.parametrize("m", [1, 3, 8])
+def test_gemm_argmax_keys(ops, dev, m):
+    """The keys epilogue: logits equal the plain GEMM bit for bit, and each
+    row's largest key names the first index of its largest bf16 logit; rows 5
+    and 700 of W are equal and dominate, so the tie goes to 5 (n = 1000 is not
+    a multiple of 16: the last group is partial)."""
+    import torch
+    rng = np.random.default_rng(40 + m)
+    n, k = 1000, 512
+    blocks = oq.make_blocks(n, k, seed=21).reshape(n, -1).copy()
+    top = blocks[5].reshape(-1, 18).copy()
+    top[:, 0:2] = np.frombuffer(np.float16(0.5).tobytes(), dtype=np.uint8)  # d = 0.5
+    top[:, 2:] = 0xFF                                                         # every nibble 15
+    blocks[5] = blocks[700] = top.reshape(-1)
+    x = f32_to_bf16_bits(np.abs(bf16_bits_to_f32(randn_bf16(rng, (m, k)))))
+    xd, wd = bf16_dev(x, dev).view(m, k), _w(blocks, dev)
+    nk = ops.gemm_keys_per_row(n)
+    assert nk == 63
+    keys = torch.zeros((m, nk), dtype=torch.int64, device=dev)
+    y = ops.q4_0_gemm_argmax(xd, wd, n, k, keys)
+    np.testing.assert_array_equal(bits_of(y), bits_of(ops.q4_0_gemm(xd, wd, n, k)))
+    kv = keys.cpu().numpy().view(np.uint64)
+    yb = bits_of(y).reshape(m, n)
+    for r in range(m):
+        best = int(kv[r].max())
+        idx = 0xFFFFFFFF - (best & 0xFFFFFFFF)
+        vals = bf16_bits_to_f32(yb[r])
+        assert idx == int(np.argmax(vals)) == 5, f"row {r}"
