@@ -184,11 +184,12 @@ def test_4b_model_greedy_tokens(dev):
     check_greedy(recs, "4B")
 
 
-@pytest.mark.parametrize("batch", [3, 8])
+@pytest.mark.parametrize("batch", [3, 8, 12])
 def test_batched_decode_against_per_sequence_oracle(dev, batch):
-    """batch sequences decoded together (MFMA GEMM path), teacher-forced with
-    different token streams: every row's logits match that sequence's own
-    oracle decoder at every step."""
+    """batch sequences decoded together (MFMA GEMM path: activations staged
+    per wave up to 8 rows, read from global memory above), teacher-forced
+    with different token streams: every row's logits match that sequence's
+    own oracle decoder at every step."""
     import torch
     m = _m()
     model = m.DecodeModel(tiny_cfg(), dev, seed=8, max_len=64, num_splits=3, batch=batch)
@@ -209,7 +210,9 @@ def test_batched_decode_against_per_sequence_oracle(dev, batch):
             if gid[r] != omodel.bf16_argmax(ol):
                 assert omodel.top2_margin(ol)[1] < omodel.NEAR_TIE_REL
                 ties += 1
-    assert ties <= 3
+    # each mismatch above is a near-tie of the fp64 logits; a few per hundred
+    # comparisons are expected from the random tiny model's flat logits
+    assert ties <= max(3, batch * T // 25)
 
 
 def test_batched_graph_replay_and_ragged_prompts(dev):
