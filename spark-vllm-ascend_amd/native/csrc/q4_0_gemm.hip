@@ -351,7 +351,7 @@ hipError_t launch_gemm_tile(hipStream_t s, const void* x, const void* w, void* y
   const int ks = ntiles < 16 ? ntiles : 16;
   const int grid = SWIGLU ? (int)((n_out + 7) / 8) : (int)((n_out + 15) / 16);
   int ws = m <= 2 ? 1 : m <= 4 ? 2 : m <= 8 ? 4 : 0;
-  if (const char* e = getenv("SMX_GEMM_WS")) ws = atoi(e) ? ws : 0;  // tuning sweeps
+  if (const char* e = tuning_env("SMX_GEMM_WS")) ws = atoi(e) ? ws : 0;  // tuning sweeps
   const size_t lds = ws ? (size_t)ks * 256 * 16 : 0;
 #define SMX_GEMM_LAUNCH(W)                                                                      \
   hipLaunchKernelGGL((q4_0_gemm_tile_kernel<SWIGLU, W, KEYS>), dim3(grid), dim3(64 * ks), lds,  \

@@ -467,8 +467,8 @@ static GemvShape pick_shape(int n_out, int out_per_group, int ngroups, int kind)
   // one shape, else SMX_GEMV_SHAPE for every shape.
   char key[64];
   snprintf(key, sizeof(key), "SMX_GEMV_SHAPE_%d_%d", n_out, ngroups);
-  const char* e = getenv(key);
-  if (!e) e = getenv("SMX_GEMV_SHAPE");
+  const char* e = tuning_env(key);
+  if (!e) e = tuning_env("SMX_GEMV_SHAPE");
   if (e) {
     int a = 0, b = 0;
     if (sscanf(e, "%d,%d", &a, &b) == 2 && (a == 1 || a == 2 || a == 4) && b >= 1 && b <= 16) {

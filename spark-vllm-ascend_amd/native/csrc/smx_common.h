@@ -1,12 +1,23 @@
 // Device helpers shared by the gfx950 kernels of the Q4_0 decode path.
 #pragma once
 
+#include <stdlib.h>
+
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 #include "../../../include/smx.h"
 
 namespace smx {
+
+// Launch-shape overrides for tuning sweeps: read only when SMX_TUNE is set
+// in the environment (looked up once per process), so a production launch
+// never calls getenv.
+inline const char* tuning_env(const char* name) {
+  static const bool on = getenv("SMX_TUNE") != nullptr;
+  return on ? getenv(name) : nullptr;
+}
+
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));

@@ -720,7 +720,7 @@ int launch_splitkv(void* stream, smx::SplitKVArgs a, int32_t num_seqs, int32_t b
     blk = 32;
     waves = 4;
   }
-  const char* e = getenv("SMX_ATTN_WAVES");  // "waves[,blk]" override for tuning sweeps
+  const char* e = smx::tuning_env("SMX_ATTN_WAVES");  // "waves[,blk]" override for tuning sweeps
   if (e) {
     int w = 0, b = 0;
     const int n = sscanf(e, "%d,%d", &w, &b);
