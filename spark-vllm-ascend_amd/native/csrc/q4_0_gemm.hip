@@ -348,8 +348,19 @@ hipError_t launch_gemm_tile(hipStream_t s, const void* x, const void* w, void* y
                             uint64_t* keys = nullptr) {
   const int npairs = (int)(k / 64);
   const int ntiles = (npairs + 3) / 4;
-  const int ks = ntiles < 16 ? ntiles : 16;
   const int grid = SWIGLU ? (int)((n_out + 7) / 8) : (int)((n_out + 15) / 16);
+  // Waves per workgroup (each takes every ks-th K tile), measured at 8 rows:
+  // many workgroups want small ones, more of them resident per CU (head
+  // 151936x2560: 4 waves 69.3 µs, 10 waves 89.7; gate/up 19456x2560: 5 waves
+  // 12.4, 10 waves 14.1), few workgroups up to 10 (down 2560x9728, 38 tiles:
+  // 10 waves 8.4, 16 waves 9.3; QKV and o_proj within 1 % from 10 to 16).
+  int ks = grid >= 4096 ? 4 : grid >= 1024 ? (ntiles + 1) / 2 : 10;
+  if (const char* e = tuning_env("SMX_GEMM_KS")) {  // tuning sweeps
+    const int v = atoi(e);
+    if (v >= 1 && v <= 16) ks = v;
+  }
+  ks = ks < 1 ? 1 : ks > 16 ? 16 : ks;
+  ks = ks < ntiles ? ks : ntiles;
   int ws = m <= 2 ? 1 : m <= 4 ? 2 : m <= 8 ? 4 : 0;
   if (const char* e = tuning_env("SMX_GEMM_WS")) ws = atoi(e) ? ws : 0;  // tuning sweeps
   const size_t lds = ws ? (size_t)ks * 256 * 16 : 0;
