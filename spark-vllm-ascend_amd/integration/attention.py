@@ -65,13 +65,14 @@ def choose_num_splits(capacity: int, tokens_per_split: int = 128, num_seqs: int 
 
 
 def choose_plan(num_seqs: int, n_kv: int = 8) -> tuple[int, int]:
-    """(num_items, num_splits) of a per-sequence split plan: one round of
-    three 4-wave workgroups per CU on a 256-CU part ((num_items + num_seqs)
-    * n_kv ~= 768), and at most 16 splits per sequence.  Measured on the
-    8-sequence step (contexts 512..32768, 115k tokens): 88 items / 16
-    splits 5.06 ms; 32 splits 5.14 ms (the merge reads num_seqs * num_splits
-    partial slots, the unused ones cleared); 56 / 120 / 184 items at 32
-    splits 5.13-5.15 / 5.19 / 5.19 ms; capacity splits 5.34 ms."""
+    """(num_items, num_splits) of a per-sequence split plan: an item budget
+    of (num_items + num_seqs) * n_kv ~= 768 workgroups and at most 16 splits
+    per sequence.  With long sequences the 16-split cap sets the split length
+    (the 8-sequence bench at contexts 512..32768: 2048-token splits, 61
+    items).  Measured there: 16 splits 5.06 ms against 5.14 with 32 (the
+    merge reads num_seqs * num_splits partial slots, the unused ones
+    cleared), 5.01 with 12 and 4.94 with 24 (2-wave workgroups); 56 / 120 /
+    184 items at 32 splits 5.13-5.19 ms; capacity splits 5.34 ms."""
     return max(1, 768 // n_kv - num_seqs), 16
 
 

@@ -713,12 +713,12 @@ int launch_splitkv(void* stream, smx::SplitKVArgs a, int32_t num_seqs, int32_t b
   int blk = tps <= 256 ? 32 : 64;
   int waves = blk == 64 ? 8 : tps <= 32 ? 1 : tps <= 64 ? 2 : tps <= 128 ? 4 : 8;
   // A plan's splits are long (the batch's tokens over a few hundred
-  // workgroups): 4 waves of 32-token blocks, three workgroups per CU (168
-  // VGPRs; 64-token blocks take 246, two workgroups per CU, and measured
-  // 4% slower on an 8-sequence step).
+  // workgroups): 2 waves of 32-token blocks per workgroup, each wave half a
+  // split (8-sequence step: 2 waves 4.69-4.72 ms, 4 waves 4.72-4.74, 1 wave
+  // 5.06; 64-token blocks take 246 VGPRs and measured 5.02).
   if (plan) {
     blk = 32;
-    waves = 4;
+    waves = 2;
   }
   const char* e = smx::tuning_env("SMX_ATTN_WAVES");  // "waves[,blk]" override for tuning sweeps
   if (e) {
