@@ -242,7 +242,8 @@ def test_plan_records_match_oracle(ops, dev, lengths, bs, items, splits):
 @pytest.mark.parametrize("lengths,bs,items,splits", [
     ([512, 3000, 77, 8192, 1, 0, 129], 128, 24, 16),
     ([512, 3000, 77, 8192, 1, 0, 129], 32, 56, 64),
-    ([6144], 128, 49, 64), ([20000], 32, 1, 1), ([9000, 40], 128, 2, 2)])
+    ([6144], 128, 49, 64), ([20000], 32, 1, 1), ([9000, 40], 128, 2, 2),
+    ([32768, 1, 20000], 128, 88, 16)])
 def test_planned_vs_fp64(ops, dev, lengths, bs, items, splits):
     """Merged outputs against float64 attention, every split's partial against
     the oracle's online softmax over the plan's bounds, and the slots no
