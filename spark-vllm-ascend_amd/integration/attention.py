@@ -59,7 +59,8 @@ def choose_num_splits(capacity: int, tokens_per_split: int = 128, num_seqs: int 
         sequences at 512..32768 tokens, 32896-token capacity: 25 splits of
         1344 tokens 5.47 ms per step, 17 / 33 splits 5.52 / 5.56 ms, 257
         splits of 128 tokens 6.14 ms): the KV stream is large, so fewer
-        workgroups, partials and merge inputs win."""
+        workgroups, partials and merge inputs win.  A per-sequence split
+        plan (choose_plan, SplitKVDecodeBackend.plan) does better still."""
     n = int(max(1, -(-capacity // tokens_per_split)))
     return min(n, 25) if num_seqs > 1 else n
 
