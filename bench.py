@@ -308,8 +308,8 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(the decode path would shard by output rows / kv heads; see DESIGN.md)",
+        print("bench.py measures one GPU: the decode path has no multi-GPU launch (it would "
+              "shard the GEMVs by output rows and the attention by kv heads)",
               file=sys.stderr)
         return 2
 

@@ -43,7 +43,7 @@ extern "C" {
 
 /* Return codes besides 0 and hipError_t values. */
 #define SMX_EINVAL 10001      /* an argument failed validation */
-#define SMX_EUNSUPPORTED 10002 /* a valid shape this build has no kernel for */
+#define SMX_EUNSUPPORTED 10002 /* a valid shape the library has no kernel for */
 
 /* ABI version of the loaded library (SMX_ABI_VERSION it was built with). */
 int smx_abi_version(void);
