@@ -62,6 +62,31 @@ def test_gemm_one_hot_layout(ops, dev, m):
     np.testing.assert_array_equal(y, exp)
 
 
+@pytest.mark.parametrize("m", [4, 7])
+@pytest.mark.parametrize("k", [64, 192, 320, 448])
+def test_gemm_partial_k_tile(ops, dev, m, k):
+    """A K tile holds 4 block pairs; with 1, 3, 5 or 7 pairs the last tile's
+    missing pairs are clamped loads that must carry no weight.  One-hot rows
+    (the first at the last column, the others spread) select dequantised
+    weights exactly; random rows match the float64 oracle.  m = 4 and 7 are
+    the last row counts of two activation staging widths."""
+    n = 40
+    blocks = oq.make_blocks(n, k, seed=k + m, scale=1.0)
+    cols = (k - 1 + 37 * np.arange(m)) % k
+    x = np.zeros((m, k), dtype=np.uint16)
+    x[np.arange(m), cols] = f32_to_bf16_bits(np.float32([1.0]))[0]
+    y = bits_of(ops.q4_0_gemm(bf16_dev(x, dev), _w(blocks, dev), n, k)).reshape(m, n)
+    exp = f32_to_bf16_bits(oq.dequant_f32(blocks, n, k)[:, cols].T.copy())
+    np.testing.assert_array_equal(y, exp)
+    rng = np.random.default_rng(k * 10 + m)
+    blocks = oq.make_blocks(200, k, seed=k + m + 1)
+    xr = randn_bf16(rng, (m, k))
+    yr = f32_of(ops.q4_0_gemm(bf16_dev(xr, dev), _w(blocks, dev), 200, k)).reshape(m, 200)
+    for r in range(m):
+        assert_close_rel(yr[r], oq.gemv_f64(xr[r], blocks, 200, k), rtol=1e-2, atol_frac=5e-3,
+                         what=f"row {r}")
+
+
 @pytest.mark.parametrize("m,d,k", [(8, 9728, 2560), (3, 100, 256), (16, 64, 512)])
 def test_gemm_swiglu(ops, dev, m, d, k):
     rng = np.random.default_rng(d + m)
