@@ -227,7 +227,8 @@ def _planned(ops, dev, q, kc, vc, table, lengths, bs, items, splits, scale,
 
 @pytest.mark.parametrize("lengths,bs,items,splits", [
     ([31075 // 8, 12494 // 8, 6639 // 8, 1, 0, 2000], 128, 24, 16),
-    ([300], 32, 56, 8), ([0, 0], 128, 8, 4), ([5000, 17], 64, 3, 2)])
+    ([300], 32, 56, 8), ([0, 0], 128, 8, 4), ([5000, 17], 64, 3, 2),
+    (list(range(0, 64 * 11, 11)), 32, 100, 8)])  # 64 sequences: every lane holds a length
 def test_plan_records_match_oracle(ops, dev, lengths, bs, items, splits):
     rng = np.random.default_rng(len(lengths) * 7 + items)
     q, kc, vc, table = _case(rng, [max(L, 1) for L in lengths], bs)
@@ -243,7 +244,7 @@ def test_plan_records_match_oracle(ops, dev, lengths, bs, items, splits):
     ([512, 3000, 77, 8192, 1, 0, 129], 128, 24, 16),
     ([512, 3000, 77, 8192, 1, 0, 129], 32, 56, 64),
     ([6144], 128, 49, 64), ([20000], 32, 1, 1), ([9000, 40], 128, 2, 2),
-    ([32768, 1, 20000], 128, 88, 16)])
+    ([32768, 1, 20000], 128, 88, 16), (list(range(0, 64 * 11, 11)), 32, 100, 8)])
 def test_planned_vs_fp64(ops, dev, lengths, bs, items, splits):
     """Merged outputs against float64 attention, every split's partial against
     the oracle's online softmax over the plan's bounds, and the slots no
