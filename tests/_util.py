@@ -56,3 +56,79 @@ def bf16_ulp_diff(a_bits: np.ndarray, b_bits: np.ndarray) -> np.ndarray:
     ka = np.where(a & 0x8000, -(a & 0x7FFF), a)
     kb = np.where(b & 0x8000, -(b & 0x7FFF), b)
     return np.abs(ka - kb)
+
+
+def bf16_bracket(v: np.ndarray, slack: np.ndarray):
+    """The bf16 values bounding [v - slack, v + slack] from outside: (lo, hi)
+    with lo <= v - slack and hi >= v + slack, each a bf16 value (float32).
+    A bf16 output of an fp32-accumulated sum whose exact value is v and whose
+    accumulation error is at most slack is lo, hi, or a bf16 value between."""
+    v = np.asarray(v, dtype=np.float64)
+    slack = np.asarray(slack, dtype=np.float64)
+
+    def step(x, up):
+        # the next bf16 value above (up) or below x, x a bf16 value (float32)
+        bits = f32_to_bf16_bits(np.asarray(x, np.float32)).astype(np.int32)
+        key = np.where(bits & 0x8000, -(bits & 0x7FFF), bits)  # monotone line
+        key = key + (1 if up else -1)
+        nb = np.where(key < 0, (-key) | 0x8000, key).astype(np.uint16)
+        return bf16_bits_to_f32(nb)
+
+    lo_t = (v - slack).astype(np.float32)
+    hi_t = (v + slack).astype(np.float32)
+    lo = bf16_bits_to_f32(f32_to_bf16_bits(lo_t))
+    lo = np.where(lo > v - slack, step(lo, False), lo)
+    hi = bf16_bits_to_f32(f32_to_bf16_bits(hi_t))
+    hi = np.where(hi < v + slack, step(hi, True), hi)
+    return lo.astype(np.float32), hi.astype(np.float32)
+
+
+def assert_swiglu_bracketed(out_f32, g_exact, u_exact, g_slack, u_slack, silu_mul, what=""):
+    """SwiGLU output of a GEMV epilogue, judged without a tolerance knob:
+    the gate and up GEMV outputs are bf16 roundings of fp32 sums, so each is a
+    bf16 value bracketing its exact (float64) value widened by the fp32
+    accumulation bound; the output must lie within 1 bf16 ulp of
+    silu_mul(g', u') over those bracketing values (silu_mul rounds to bf16)."""
+    g_lo, g_hi = bf16_bracket(g_exact, g_slack)
+    u_lo, u_hi = bf16_bracket(u_exact, u_slack)
+    cands = np.stack([silu_mul(g, u) for g in (g_lo, g_hi) for u in (u_lo, u_hi)])
+    c_bits = f32_to_bf16_bits(cands.astype(np.float32))
+    o_bits = f32_to_bf16_bits(np.asarray(out_f32, np.float32))
+    key = lambda b: np.where(b.astype(np.int32) & 0x8000, -(b.astype(np.int32) & 0x7FFF),
+                             b.astype(np.int32))
+    ok = (key(o_bits) >= key(c_bits).min(axis=0) - 1) & (key(o_bits) <= key(c_bits).max(axis=0) + 1)
+    if not ok.all():
+        i = int(np.argmin(ok))
+        raise AssertionError(
+            f"{what}: {int((~ok).sum())}/{ok.size} outside the bracket; at {i}: out "
+            f"{float(np.asarray(out_f32).flat[i])!r}, candidates {cands[:, i].tolist()}, "
+            f"g {float(g_exact.flat[i])!r} u {float(u_exact.flat[i])!r}")
+
+
+def gemv_abs_sum(x_bits: np.ndarray, blocks: np.ndarray, n: int, k: int) -> np.ndarray:
+    """sum_j |x_j| |w_ij| per output row (float64): the scale of an fp32
+    accumulation's rounding error for that row."""
+    from oracle import q4_0 as oq
+    w = np.abs(oq.dequant_f32(blocks, n, k))
+    return w.astype(np.float64) @ np.abs(bf16_bits_to_f32(x_bits).astype(np.float64))
+
+
+# Slack granted to an fp32-accumulated dot product, relative to its row's
+# absolute sum (the per-block dot2 chains run at about 34x the magnitude of
+# their result, so 2^-18 is a few hundred fp32 ulps of the result's scale).
+FP32_ACC_SLACK = 2.0 ** -18
+
+
+def assert_faithful_bf16(got_f32, exact, slack, what=""):
+    """Every output is one of the bf16 values bracketing its exact value
+    (widened by slack): the bf16 rounding of an accumulation whose error is
+    below slack, at most one ulp from the exact value's own rounding."""
+    lo, hi = bf16_bracket(exact, slack)
+    got = np.asarray(got_f32, np.float32)
+    ok = (got >= lo) & (got <= hi)
+    if not ok.all():
+        i = int(np.argmin(ok))
+        raise AssertionError(f"{what}: {int((~ok).sum())}/{ok.size} outside the bf16 bracket; "
+                             f"at {i}: got {float(got.flat[i])!r} exact "
+                             f"{float(np.asarray(exact).flat[i])!r} bracket "
+                             f"[{float(lo.flat[i])!r}, {float(hi.flat[i])!r}]")

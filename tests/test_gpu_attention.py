@@ -64,8 +64,6 @@ def _run(ops, dev, q, kc, vc, table, lengths, splits, scale, merged=False):
 @pytest.mark.parametrize("L", [1, 2, 31, 32, 33, 127, 128, 129, 300, 2048, 4096, 6144])
 @pytest.mark.parametrize("splits", [1, 4, 8, 16, 32, 64])
 def test_splitkv_vs_fp64(ops, dev, L, splits, merged):
-    if L > 2048 and splits in (1, 4) and L != 6144:
-        pytest.skip("covered by other split counts")
     rng = np.random.default_rng(L * 31 + splits)
     bs = 128
     q, kc, vc, table = _case(rng, [L], bs)

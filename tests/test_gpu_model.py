@@ -4,10 +4,11 @@
     at every teacher-forced step, greedy tokens equal except near-ties;
   * graph replay equals eager execution bit for bit;
   * one full-size layer (hidden 2560, 32q/8kv, intermediate 9728) at context
-    4096 against the oracle layer;
+    4096 against the oracle layer, within 1e-2;
   * the 36-layer 4B-shape model: greedy tokens teacher-forced against the
     oracle, disagreements only at near-ties (float64 top-2 margin below 2e-2
-    of the top logit).
+    of the top logit), from an empty cache and at contexts 2048-2051 and
+    4093-4096 over a seeded cache (the contexts a decode benchmark times).
 """
 import numpy as np
 import pytest
@@ -115,45 +116,45 @@ def test_graph_replay_matches_eager(dev):
 
 
 @pytest.mark.parametrize("fused", [True, False])
-def test_full_size_layer_at_4096(dev, fused):
+@pytest.mark.parametrize("seed", [7, 8])
+def test_full_size_layer_at_4096(dev, fused, seed):
+    """One full-size layer (hidden 2560, 32q/8kv, SwiGLU 9728) at position
+    4095 over a seeded cache, against the oracle layer, at the 1e-2 bar:
+    elementwise within 1e-2 relative plus 1e-2 of the output rms, and within
+    1e-2 in relative L2.  Measured on MI355X (seeds 7-9, both paths): relative
+    L2 3.2-3.7e-3, the largest error 1.4-2.2e-2 of the rms -- bf16 outputs of
+    two implementations whose GEMVs accumulate in different orders differ by
+    one ulp at about half the elements of each stage (0.39% of an element),
+    and a residual element near zero carries the absolute part."""
     import torch
     m = _m()
     cfg = m.DecoderConfig(n_layers=1, vocab=512)
     L = 4096
-    model = m.DecodeModel(cfg, dev, seed=7, max_len=L + 128, num_splits=16, fused=fused)
+    model = m.DecodeModel(cfg, dev, seed=seed, max_len=L + 128, num_splits=16, fused=fused)
     oracle = oracle_from(model, num_splits=16)
-    rng = np.random.default_rng(7)
     pos = L - 1
-    # fill the cache for positions < pos through the block table
-    kv = model.layers[0].kv_cache
+    fill_kv(model, oracle, pos, seed)  # positions < pos
     table = model.state.block_table[0].cpu().numpy()
-    kf = rng.standard_normal((pos, cfg.n_kv, cfg.head_dim)).astype(np.float32)
-    vf = rng.standard_normal((pos, cfg.n_kv, cfg.head_dim)).astype(np.float32)
-    kb = torch.from_numpy(kf).to(torch.bfloat16)
-    vb = torch.from_numpy(vf).to(torch.bfloat16)
-    for t0 in range(0, pos, cfg.block_size):
-        t1 = min(pos, t0 + cfg.block_size)
-        page = int(table[t0 // cfg.block_size])
-        kv[0, page, :t1 - t0] = kb[t0:t1].to(dev)
-        kv[1, page, :t1 - t0] = vb[t0:t1].to(dev)
     st = model.state
     st.positions.fill_(pos)
     st.seq_lens.fill_(pos + 1)
     st.slot_mapping.fill_(int(table[pos // cfg.block_size]) * cfg.block_size + pos % cfg.block_size)
-    x = (3 * torch.randn((1, cfg.hidden))).to(torch.bfloat16)  # layer 0 input: the embedding
+    x = (3 * torch.randn((1, cfg.hidden), generator=torch.Generator().manual_seed(seed))).to(
+        torch.bfloat16)  # layer 0 input: the embedding
     model.x.copy_(x.to(dev))
     model.layer_run(0)
     # the next consumer (here the head) adds and normalises (down, residual)
     y_dev, r_dev = pkg("native.torch_ops").add_rmsnorm(model.d, model.res_b, model.final_norm,
                                                        cfg.eps)
     torch.cuda.synchronize()
-    oracle.k[0] = kb.float().numpy()
-    oracle.v[0] = vb.float().numpy()
     xf = x.float().numpy()[0]
     h0, _ = oops.add_rmsnorm(xf, None, f32_of(model.layers[0].input_norm), cfg.eps)
     y, res = oracle.layer(0, h0, xf, pos)
-    assert_close_rel(f32_of(r_dev).reshape(-1), res, rtol=2e-2, atol_frac=2e-2, what="residual")
-    assert_close_rel(f32_of(y_dev).reshape(-1), y, rtol=5e-2, atol_frac=5e-2, what="layer out")
+    for what, got, ref in (("residual", f32_of(r_dev).reshape(-1), res),
+                           ("layer out", f32_of(y_dev).reshape(-1), y)):
+        assert_close_rel(got, ref, rtol=1e-2, atol_frac=1e-2, what=what)
+        rel_l2 = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+        assert rel_l2 < 1e-2, f"{what}: relative L2 {rel_l2:.3g}"
 
 
 @pytest.mark.parametrize("num_splits", [2, 3])
@@ -182,6 +183,60 @@ def test_4b_model_greedy_tokens(dev):
     seq = rng.integers(0, model.cfg.vocab, 6)
     recs = teacher_forced(model, oracle, seq)
     check_greedy(recs, "4B")
+
+
+def fill_kv(model, oracle, length: int, seed: int) -> None:
+    """Seeded N(0,1) bf16 K and V for positions < length in every layer,
+    written through the model's block table (row 0) and given to the oracle
+    as its cache."""
+    import torch
+    c = model.cfg
+    bs = c.block_size
+    pages = model.state.block_table[0, :(length + bs - 1) // bs].long()
+    g = torch.Generator(device=model.device).manual_seed(seed)
+    for i, L in enumerate(model.layers):
+        kv = torch.randn((2, pages.numel() * bs, c.n_kv, c.head_dim), generator=g,
+                         device=model.device).to(torch.bfloat16)
+        kv[:, length:] = 0
+        L.kv_cache[:, pages] = kv.view(2, pages.numel(), bs, c.n_kv, c.head_dim)
+        host = kv[:, :length].float().cpu().numpy()
+        oracle.k[i] = host[0]
+        oracle.v[i] = host[1]
+
+
+@pytest.mark.parametrize("start", [2048, 4093])
+def test_4b_model_teacher_forced_at_long_context(dev, start):
+    """The 36-layer 4B model at the contexts a decode benchmark times (the
+    2048-token prompt's KV in the cache, then four teacher-forced tokens, and
+    again near 4096): every step's logits against the float64 oracle decoder
+    holding the same cache, greedy tokens equal except at near-ties.  The
+    block table's capacity is 6144 tokens (48 splits of 128), as in the
+    benchmark."""
+    import torch
+    m = _m()
+    model = m.DecodeModel(m.DecoderConfig(), dev, seed=2, max_len=6144)
+    oracle = oracle_from(model, num_splits=model.num_splits)
+    fill_kv(model, oracle, start, seed=start)
+    T = 4
+    seq = np.random.default_rng(start).integers(0, model.cfg.vocab, T)
+    st = model.state
+    model.set_context([start], ids=[int(seq[0])])
+    st.forced[0, start + 1:start + T] = torch.from_numpy(seq[1:]).to(dev)
+    st.forced_len.fill_(start + T)
+    model.capture()
+    model.set_context([start], ids=[int(seq[0])])
+    st.forced_len.fill_(start + T)
+    recs = []
+    for j in range(T):
+        model.step()
+        torch.cuda.synchronize()
+        gl = f32_of(model.logits).reshape(-1)
+        gid = int(st.next_ids.item())
+        recs.append((gid, oracle.step(int(seq[j]), start + j), gl))
+        print(f"4B ctx {start + j}: step checked", flush=True)
+    # the tokens fed are the forced ones, by position
+    np.testing.assert_array_equal(st.tokens[0, start + 1:start + T].cpu().numpy(), seq[1:])
+    check_greedy(recs, f"4B at {start}")
 
 
 @pytest.mark.parametrize("batch", [3, 8, 12])

@@ -1,7 +1,10 @@
 """GPU parity of the Q4_0 kernels (dequant, GEMV, GEMV+SwiGLU) against the
 oracle, through the C ABI.  Bars: dequantisation bit-exact; GEMV within 1e-2
 relative of the float64 oracle (plus 1e-3 of the row RMS for cancellation),
-and at least 95% of outputs equal to the bf16 rounding of the fp64 result."""
+at least 95% of outputs equal to the bf16 rounding of the fp64 result, and
+every output one of the two bf16 values bracketing the exact result (an fp32
+accumulation's slack added); SwiGLU within 1 bf16 ulp of silu(g) * u over
+the bf16 values bracketing the exact gate and up outputs."""
 import numpy as np
 import pytest
 
@@ -9,7 +12,8 @@ from oracle import q4_0 as oq
 from oracle.bf16 import bf16_bits_to_f32, f32_to_bf16_bits
 from oracle.ops import silu_mul as o_silu_mul
 
-from _util import assert_close_rel, bf16_dev, bits_of, f32_of, pkg, randn_bf16
+from _util import (FP32_ACC_SLACK, assert_close_rel, assert_faithful_bf16, assert_swiglu_bracketed,
+                   bf16_dev, bits_of, f32_of, gemv_abs_sum, pkg, randn_bf16)
 
 pytestmark = pytest.mark.gpu
 
@@ -78,6 +82,8 @@ def test_gemv_vs_oracle(ops, dev, n, k):
     assert_close_rel(got, ref, what=f"gemv {n}x{k}")
     same = np.mean(got_bits == f32_to_bf16_bits(ref.astype(np.float32)))
     assert same >= 0.95, f"only {same:.3f} of outputs equal bf16(fp64 oracle)"
+    assert_faithful_bf16(got, ref, FP32_ACC_SLACK * gemv_abs_sum(x_bits, blocks, n, k),
+                         what=f"gemv {n}x{k}")
 
 
 def test_gemv_lm_head_shape(ops, dev):
@@ -138,11 +144,10 @@ def test_gemv_swiglu(ops, dev, d, k):
     blocks = oq.make_blocks(2 * d, k, seed=d)
     x_bits = randn_bf16(rng, k)
     out = ops.q4_0_gemv_swiglu(bf16_dev(x_bits, dev), _blocks_dev(blocks, dev), d, k)
-    ref_gu = oq.gemv_f64(x_bits, blocks, 2 * d, k).astype(np.float32)
-    g = bf16_bits_to_f32(f32_to_bf16_bits(ref_gu[:d]))
-    u = bf16_bits_to_f32(f32_to_bf16_bits(ref_gu[d:]))
-    ref = o_silu_mul(g, u)
-    assert_close_rel(f32_of(out).reshape(d), ref, rtol=2e-2, atol_frac=5e-3, what="swiglu")
+    gu = oq.gemv_f64(x_bits, blocks, 2 * d, k)
+    slack = FP32_ACC_SLACK * gemv_abs_sum(x_bits, blocks, 2 * d, k)
+    assert_swiglu_bracketed(f32_of(out).reshape(d), gu[:d], gu[d:], slack[:d], slack[d:],
+                            o_silu_mul, what=f"swiglu {d}x{k}")
 
 
 def test_gemv_rejects_bad_arguments(ops, dev):

@@ -142,6 +142,35 @@ def test_gemv_one_hot_and_linearity_and_zero_scale():
     assert not oq.gemv_f64(a, zero.reshape(n, -1), n, k).any()
 
 
+def test_gemv_bf16_weight_rounding_kat():
+    """gemv_bf16w_bits rounds each weight d * q to bf16 before the product
+    (sva/kernels/linear.py:87-100).  Rows of 8 blocks with x = 1: blocks 0-3
+    hold q = +1 (nibble 9) at an fp16 scale d that is not a bf16 value, blocks
+    4-7 hold q = -1 at d = 1 (exact), so the row sum is 128 * (bf16(d) - 1)
+    with weight rounding and 128 * (d - 1) without.
+      d = 1 + 3 * 2^-10: bf16(d) = 1         -> 0       (exact 0.375)
+      d = 1 + 5 * 2^-10: bf16(d) = 1 + 2^-7  -> 1.0     (exact 0.625)
+      d = 1 + 4 * 2^-10: a tie, to even = 1  -> 0       (exact 0.5)
+      d = 1 + 2^-7 (bf16-exact)              -> 1.0     (exact 1.0)
+    A GEMV that skipped the weight rounding, or rounded ties away from zero,
+    gives different bits."""
+    n, k = 4, 256
+    scales = [1 + 3 * 2.0 ** -10, 1 + 5 * 2.0 ** -10, 1 + 4 * 2.0 ** -10, 1 + 2.0 ** -7]
+    d = np.empty((n, 8), dtype=np.float16)
+    codes = np.empty((n, 8, 32), dtype=np.uint8)
+    for r, s in enumerate(scales):
+        d[r, :4] = s
+        d[r, 4:] = 1.0
+        codes[r, :4] = 9
+        codes[r, 4:] = 7
+    assert all(float(np.float16(s)) == s for s in scales)  # fp16-exact scales
+    blocks = oq.pack_blocks(d, codes)
+    x = np.full(k, 0x3F80, dtype=np.uint16)  # 1.0
+    got = bf16_bits_to_f32(oq.gemv_bf16w_bits(x, blocks, n, k))
+    np.testing.assert_array_equal(got, np.float32([0.0, 1.0, 0.0, 1.0]))
+    np.testing.assert_array_equal(oq.gemv_f64(x, blocks, n, k), [0.375, 0.625, 0.5, 1.0])
+
+
 def test_gemv_bf16_weight_variant_close_to_exact():
     rng = np.random.default_rng(3)
     n, k = 64, 2560
