@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define SMX_ABI_VERSION 4
+#define SMX_ABI_VERSION 5
 
 /* Return codes besides 0 and hipError_t values. */
 #define SMX_EINVAL 10001      /* an argument failed validation */
@@ -167,6 +167,29 @@ int smx_splitkv_decode_merged(void* stream, const void* q, const void* k_cache,
                               int32_t num_splits, int32_t max_blocks,
                               int32_t num_blocks, int32_t block_size, int32_t n_q,
                               int32_t n_kv, int32_t head_dim, float scale);
+
+/*
+ * smx_splitkv_decode_merged without caller workspace, for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  No counterpart in the reference.
+ * The split partials live in a fixed device array of SMX_NOALLOC_SCRATCH_BYTES
+ * inside the library (one per GPU, held until the process ends); the call
+ * allocates nothing.  It needs
+ *   num_seqs * num_splits * n_q * 4 * head_dim  (rounded up to 256)
+ *   + num_seqs * num_splits * n_q * 4  <=  SMX_NOALLOC_SCRATCH_BYTES
+ * bytes (at n_q 32, head_dim 128: 16,512 per (sequence, split), 508 of them),
+ * else SMX_EINVAL.  Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (two streams, concurrent graph replays) race.  The first
+ * call on a device resolves the array's device address there.
+ * Same arguments and result as smx_splitkv_decode_merged otherwise.
+ */
+#define SMX_NOALLOC_SCRATCH_BYTES (8u << 20)
+int smx_splitkv_decode_merged_noalloc(void* stream, const void* q, const void* k_cache,
+                                      const void* v_cache, const int32_t* block_table,
+                                      const int32_t* seq_lens, void* out, int32_t num_seqs,
+                                      int32_t num_splits, int32_t max_blocks,
+                                      int32_t num_blocks, int32_t block_size, int32_t n_q,
+                                      int32_t n_kv, int32_t head_dim, float scale);
 
 /*
  * smx_qknorm_rope_kv_write fused into smx_splitkv_decode_merged, for one

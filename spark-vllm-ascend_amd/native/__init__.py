@@ -16,7 +16,7 @@ import ctypes
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libsmx.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 SMX_EINVAL = 10001
 SMX_EUNSUPPORTED = 10002
 
@@ -35,6 +35,8 @@ SIGNATURES = {
                            _I32, _I32, _F32],
     "smx_splitkv_decode_merged": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32,
                                   _I32, _I32, _I32, _I32, _F32],
+    "smx_splitkv_decode_merged_noalloc": [_P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32,
+                                          _I32, _I32, _I32, _I32, _F32],
     "smx_qknorm_rope_splitkv_decode_merged": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                               _P, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32,
                                               _I32, _F32, _F32],

@@ -21,6 +21,8 @@
 // more than a launch.
 #include <math.h>
 
+#include <mutex>
+
 #include "smx_common.h"
 
 namespace smx {
@@ -839,6 +841,92 @@ extern "C" int smx_splitkv_decode_merged(void* stream, const void* q, const void
                                        num_seqs, block_size, scale);
   if (rc) return rc;
   return launch_merge(stream, partial_o, partial_lse, out, num_seqs, num_splits, n_q);
+}
+
+// ---------------------------------------------------------------------------
+// smx_splitkv_decode_merged_noalloc: the same two launches, with the split
+// partials in a file-scope device array instead of caller buffers, for callers
+// that cannot allocate.  Every GPU the library runs on holds its own copy of
+// the array until the process ends.  In host code `scratch` names a host-side
+// stand-in, not device memory: its device address comes from
+// hipGetSymbolAddress, once per device (with that device current), and only
+// that address is handed to kernels.  All calls on one GPU share the array,
+// so calls that overlap on one GPU (different streams, or graphs replayed
+// concurrently) race.  Nothing needs clearing between calls: the decode
+// kernel writes every (sequence, split) slot the merge reads, an empty split
+// included.
+// ---------------------------------------------------------------------------
+namespace {
+static __device__ __align__(256) unsigned char scratch[SMX_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of this device's scratch array (resolved on first use), or
+// nullptr with *rc set to the HIP error.
+void* scratch_for_current_device(int* rc) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    *rc = (int)e;
+    return nullptr;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    *rc = (int)hipErrorInvalidDevice;
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      *rc = e != hipSuccess ? (int)e : (int)hipErrorInvalidSymbol;
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  return g_scratch_ptr[dev];
+}
+
+// Bytes of scratch a call uses: the partials, then (256-byte aligned) the lse.
+int64_t noalloc_bytes(int32_t num_seqs, int32_t num_splits, int32_t n_q, int32_t head_dim) {
+  if (num_seqs < 1 || num_splits < 1 || n_q < 1 || head_dim < 1) return -1;
+  const int64_t slots = (int64_t)num_seqs * num_splits * n_q;
+  const int64_t o_bytes = (slots * head_dim * 4 + 255) / 256 * 256;
+  return o_bytes + slots * 4;
+}
+}  // namespace
+
+extern "C" int smx_splitkv_decode_merged_noalloc(void* stream, const void* q, const void* k_cache,
+                                                 const void* v_cache, const int32_t* block_table,
+                                                 const int32_t* seq_lens, void* out,
+                                                 int32_t num_seqs, int32_t num_splits,
+                                                 int32_t max_blocks, int32_t num_blocks,
+                                                 int32_t block_size, int32_t n_q, int32_t n_kv,
+                                                 int32_t head_dim, float scale) {
+  // the partial pointers are checked below, once the scratch address is known
+  const float* partial_o = reinterpret_cast<const float*>(16);
+  const float* partial_lse = partial_o;
+  SMX_SPLITKV_CHECKS();
+  SMX_REQUIRE(out && (uintptr_t)out % 2 == 0, "out must be non-null and 2-byte aligned");
+  const int64_t need = noalloc_bytes(num_seqs, num_splits, n_q, head_dim);
+  SMX_REQUIRE(need > 0 && need <= (int64_t)SMX_NOALLOC_SCRATCH_BYTES,
+              "num_seqs * num_splits * n_q * (4 * head_dim + 4) bytes (with the lse block "
+              "256-byte aligned) exceed SMX_NOALLOC_SCRATCH_BYTES; use "
+              "smx_splitkv_decode_merged with caller buffers");
+  int rc = 0;
+  unsigned char* base = static_cast<unsigned char*>(scratch_for_current_device(&rc));
+  if (!base) return rc;
+  const int64_t o_bytes = need - (int64_t)num_seqs * num_splits * n_q * 4;
+  float* po = reinterpret_cast<float*>(base);
+  float* pl = reinterpret_cast<float*>(base + o_bytes);
+  rc = launch_splitkv<false>(stream,
+                             splitkv_args(q, k_cache, v_cache, block_table, seq_lens, po, pl,
+                                          num_splits, max_blocks, num_blocks, n_q, n_kv),
+                             num_seqs, block_size, scale);
+  if (rc) return rc;
+  return launch_merge(stream, po, pl, out, num_seqs, num_splits, n_q);
 }
 
 extern "C" int smx_qknorm_rope_splitkv_decode_merged(
