@@ -2,12 +2,20 @@
 
 Workload (the configuration the headline metric is quoted on): 36-layer
 decoder, hidden 2560, 32 q / 8 kv heads of 128, SwiGLU 9728, tied vocab
-151936 with a Q4_0 head, random-init weights, BF16 paged KV (block 128).
-A 2048-token random prompt is fed through the decode graph, the first
-generated token is the untimed warmup, and K further greedy tokens are timed:
-TPOT = time / K, as the reference defines it over SSE events
-((t_last - t_first) / 4095, src/tools/benchmark/benchmark.py:123).  The
-median over --runs independent runs is reported.
+151936 with a Q4_0 head, random-init weights, BF16 paged KV (block 128) over a
+block table of 49 pages (6272 tokens: the 2048 + 4096 tokens of the protocol,
+whatever --steps is, so the kernels' split count does not follow the run's
+length).  TPOT is the reference's: time per generated token after the first
+((t_last - t_first) / 4095, src/tools/benchmark/benchmark.py:123).
+  --steps 4095 (the default): the protocol itself -- a 2048-token random
+      prompt fed through the captured decode graph, the first generated token
+      untimed, the next 4095 timed.
+  --steps K < 4095: K timed tokens spread over the protocol's contexts --
+      up to 4 segments starting at contexts from 2049 to 6144 - K/4, each
+      after --warmup untimed tokens, over a KV cache pre-filled with seeded
+      random bf16 -- so a short run reports the protocol's mean context, not
+      its first tokens.
+The median over --runs independent runs is reported.
 
 Also reported, on the same box in the same run:
   roofline      the Q4_0 GEMV [9728 x 2560] (the dominant kernel class:
@@ -15,11 +23,17 @@ Also reported, on the same box in the same run:
                 over a captured graph of launches that rotate through 24
                 weight sets (336 MB, larger than the 256 MB Infinity Cache);
                 achieved = 14,032,896 algorithmic bytes / mean launch time;
-  attention     split-KV decode + LSE merge at context 6144 (25.2 MB of KV)
-                over 12 rotating KV sets, for each split count;
+                ceiling = a streaming-read kernel over the same weight sets;
+  attention     split-KV decode + LSE merge at contexts 2048 / 4096 / 6144
+                over rotating KV sets (> 256 MB), for each split count, with
+                the streaming-read ceiling of the same bytes;
   step          bytes a decode step streams vs the HBM-bound step time;
-  cpu_baseline  the reference's PyTorch CPU path (bf16 weights, F.linear)
-                on this host's cores, on a bounded sample of decode steps.
+  batch_decode  8 sequences at seeded ragged contexts in one step;
+  cpu_baseline  the reference's PyTorch CPU path (bf16 weights, F.linear) on
+                this host's cores: decode steps on all cores and on 4 threads
+                (the reference's OMP_NUM_THREADS=4), the single GEMV
+                (F.linear and the fp32-accumulating restatement), and split-free
+                fp32 attention at 6144.
 One JSON line is printed.
 """
 from __future__ import annotations
@@ -37,8 +51,13 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 GEMV_N, GEMV_K = 9728, 2560
-GEMV_BYTES = GEMV_N * GEMV_K // 32 * 18 + GEMV_K * 2 + GEMV_N * 2  # 14,032,896
-ATTN_CTX = 6144
+GEMV_W_BYTES = GEMV_N * GEMV_K // 32 * 18                # 14,008,320
+GEMV_BYTES = GEMV_W_BYTES + GEMV_K * 2 + GEMV_N * 2      # 14,032,896
+ATTN_CTXS = (2048, 4096, 6144)
+ATTN_SPLITS = (4, 8, 16, 32, 48, 64)
+ROTATE_BYTES = 300 << 20    # rotating sets exceed the 256 MB Infinity Cache
+PROMPT, GENERATED = 2048, 4096
+CAPACITY = 6272             # 49 pages of 128: the protocol's 6144 tokens + the last token id
 
 
 def log(msg: str) -> None:
@@ -70,6 +89,29 @@ def time_graph(fn, launches_per_call: int, reps: int, warm: int = 2):
     return start.elapsed_time(end) * 1e3 / (reps * launches_per_call)
 
 
+def read_ceiling(bufs, nbytes: int, reps: int):
+    """Streaming-read ceiling of `nbytes` per launch over the rotating buffers
+    `bufs` (16-byte aligned device tensors of at least nbytes): the fastest
+    loads-per-lane setting of the read probe, timed like the kernels."""
+    import torch
+    from spark_vllm_ascend_amd.native import torch_ops as ops
+    best = None
+    for loads in (2, 4, 8, 16):
+        sink = torch.empty(ops.read_probe_sink_size(nbytes, loads), dtype=torch.int32,
+                           device=bufs[0].device)
+
+        def fn():
+            for b in bufs:
+                ops.read_probe(b, nbytes, sink, loads)
+        us = time_graph(fn, len(bufs), reps)
+        if best is None or us < best[0]:
+            best = (us, loads)
+    us, loads = best
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {"bytes": nbytes, "us": round(us, 3), "gbs": round(gbs, 1),
+            "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4), "loads_per_lane": loads}
+
+
 def gemv_roofline(dev, reps: int):
     import torch
     from spark_vllm_ascend_amd.integration.weights import synthetic_q4_0
@@ -84,51 +126,69 @@ def gemv_roofline(dev, reps: int):
             ops.q4_0_gemv(x, w, GEMV_N, GEMV_K, out=y)
     us = time_graph(fn, sets, reps)
     gbs = GEMV_BYTES / (us * 1e-6) / 1e9
+    ceil = read_ceiling([w.view(-1) for w in ws], GEMV_W_BYTES, reps)
     del ws
     return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+            "ceiling_gbs": ceil["gbs"], "frac_of_ceiling": round(gbs / ceil["gbs"], 4),
+            "ceiling": ceil,
             "kernel": "q4_0_gemv_kernel (Q4_0 GEMV 9728x2560, x bf16, y bf16)",
             "bytes_per_launch": GEMV_BYTES, "us_per_launch": round(us, 3),
             "timing": "HIP events over a captured graph of 24 launches on rotating weight sets "
-                      "(336 MB), mean per launch including dispatch gaps"}
+                      "(336 MB), mean per launch including dispatch gaps; ceiling: the "
+                      "streaming-read probe over the same 24 weight buffers"}
 
 
-def attention_roofline(dev, reps: int, splits_list=(4, 8, 16, 32, 64)):
+def attention_roofline(dev, reps: int, ctxs=ATTN_CTXS, splits_list=ATTN_SPLITS):
     import torch
     from spark_vllm_ascend_amd.native import torch_ops as ops
     n_q, n_kv, hd, bs = 32, 8, 128, 128
-    nblk = ATTN_CTX // bs
-    sets = 12
-    g = torch.Generator(device=dev).manual_seed(7)
-    caches = []
-    for _ in range(sets):
-        kc = torch.randn((nblk, bs, n_kv, hd), generator=g, device=dev).to(torch.bfloat16)
-        vc = torch.randn((nblk, bs, n_kv, hd), generator=g, device=dev).to(torch.bfloat16)
-        caches.append((kc, vc))
-    table = torch.randperm(nblk, generator=torch.Generator().manual_seed(3)).to(torch.int32)
-    table = table.view(1, -1).to(dev)
-    q = torch.randn((1, n_q, hd), device=dev).to(torch.bfloat16)
-    seq_lens = torch.tensor([ATTN_CTX], dtype=torch.int32, device=dev)
-    out = torch.empty((1, n_q, hd), dtype=torch.bfloat16, device=dev)
-    algo = 2 * ATTN_CTX * n_kv * hd * 2 + 2 * n_q * hd * 2  # K+V + q + out = 25,182,208
-    res = {}
-    for S in splits_list:
-        po = torch.empty((1, S, n_q, hd), dtype=torch.float32, device=dev)
-        pl = torch.empty((1, S, n_q), dtype=torch.float32, device=dev)
+    out = {}
+    for ctx in ctxs:
+        nblk = ctx // bs
+        kv_bytes = 2 * ctx * n_kv * hd * 2
+        sets = max(2, -(-ROTATE_BYTES // kv_bytes))
+        g = torch.Generator(device=dev).manual_seed(7)
+        planes = []  # K and V of one set in one allocation (the ceiling reads both at once)
+        for _ in range(sets):
+            kv = torch.empty((2, nblk, bs, n_kv, hd), dtype=torch.bfloat16, device=dev)
+            kv.normal_(generator=g)
+            planes.append(kv)
+        caches = [(kv[0], kv[1]) for kv in planes]
+        table = torch.randperm(nblk, generator=torch.Generator().manual_seed(3)).to(torch.int32)
+        table = table.view(1, -1).to(dev)
+        q = torch.randn((1, n_q, hd), device=dev).to(torch.bfloat16)
+        seq_lens = torch.tensor([ctx], dtype=torch.int32, device=dev)
+        o = torch.empty((1, n_q, hd), dtype=torch.bfloat16, device=dev)
+        algo = kv_bytes + 2 * n_q * hd * 2  # K+V + q + out
+        res = {}
+        for S in splits_list:
+            po = torch.empty((1, S, n_q, hd), dtype=torch.float32, device=dev)
+            pl = torch.empty((1, S, n_q), dtype=torch.float32, device=dev)
 
-        def fn():
-            for kc, vc in caches:
-                ops.splitkv_decode_merged(q, kc, vc, table, seq_lens, S, hd ** -0.5, po, pl,
-                                          out=out)
-        us = time_graph(fn, sets, reps)
-        gbs = algo / (us * 1e-6) / 1e9
-        res[S] = {"us": round(us, 3), "achieved_gbs": round(gbs, 1),
-                  "frac": round(gbs / HBM_PEAK_GBS, 4)}
-    best = min(res, key=lambda s: res[s]["us"])
-    del caches
-    return {"ctx": ATTN_CTX, "bytes_per_call": algo, "best_splits": best, **res[best],
-            "sweep": res, "timing": "split-KV kernel + LSE merge kernel per call, HIP events "
-                                   "over a graph of 12 calls on rotating KV sets (302 MB)"}
+            def fn():
+                for kc, vc in caches:
+                    ops.splitkv_decode_merged(q, kc, vc, table, seq_lens, S, hd ** -0.5, po, pl,
+                                              out=o)
+            us = time_graph(fn, sets, reps)
+            gbs = algo / (us * 1e-6) / 1e9
+            res[S] = {"us": round(us, 3), "achieved_gbs": round(gbs, 1),
+                      "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        best = min(res, key=lambda s: res[s]["us"])
+        # the read ceiling over the same bytes: each set's K and V read in one launch
+        ceil = read_ceiling([kv.view(-1) for kv in planes], kv_bytes, reps)
+        out[ctx] = {"bytes_per_call": algo, "sets": sets, "best_splits": best, **res[best],
+                    "ceiling_gbs": ceil["gbs"], "ceiling_us": ceil["us"],
+                    "frac_of_ceiling": round(algo / (res[best]["us"] * 1e-6) / 1e9 / ceil["gbs"], 4),
+                    "sweep": res}
+        del caches, planes
+        torch.cuda.empty_cache()
+    return {"by_ctx": out, "ctx": 6144, **{k: out[6144][k] for k in
+                                           ("bytes_per_call", "best_splits", "us",
+                                            "achieved_gbs", "frac", "ceiling_gbs")},
+            "timing": "split-KV kernel + LSE merge kernel per call, HIP events over a graph of "
+                      "calls on rotating KV sets (> 300 MB per context); ceiling: the "
+                      "streaming-read probe over the same K and V planes"}
 
 
 COPY_BYTES = 64 << 20
@@ -138,7 +198,8 @@ def counter_workload(dev):
     """Eager launches for a hardware-counter run (rocprofv3 --pmc): a plain
     device copy of COPY_BYTES (the calibration kernel: it reads and writes
     exactly COPY_BYTES), then the 9728x2560 GEMV over 24 rotating weight
-    sets, then split-KV decode + merge at context 6144 over 12 KV sets."""
+    sets, then split-KV decode + merge at context 6144 over 12 KV sets, then
+    the streaming-read probe over the GEMV's weight sets."""
     import torch
     from spark_vllm_ascend_amd.integration.weights import synthetic_q4_0
     from spark_vllm_ascend_amd.native import torch_ops as ops
@@ -154,24 +215,28 @@ def counter_workload(dev):
         for w in ws:
             ops.q4_0_gemv(x, w, GEMV_N, GEMV_K, out=y)
     torch.cuda.synchronize()
+    sink = torch.empty(ops.read_probe_sink_size(GEMV_W_BYTES, 8), dtype=torch.int32, device=dev)
+    for w in ws:
+        ops.read_probe(w.view(-1), GEMV_W_BYTES, sink, 8)
+    torch.cuda.synchronize()
     del ws
     n_q, n_kv, hd, bs = 32, 8, 128, 128
-    nblk = ATTN_CTX // bs
+    nblk = 6144 // bs
     caches = [(torch.randn((nblk, bs, n_kv, hd), device=dev).to(torch.bfloat16),
                torch.randn((nblk, bs, n_kv, hd), device=dev).to(torch.bfloat16))
               for _ in range(12)]
     table = torch.randperm(nblk, generator=torch.Generator().manual_seed(3)).to(torch.int32)
     table = table.view(1, -1).to(dev)
     q = torch.randn((1, n_q, hd), device=dev).to(torch.bfloat16)
-    seq_lens = torch.tensor([ATTN_CTX], dtype=torch.int32, device=dev)
-    S = 32
+    seq_lens = torch.tensor([6144], dtype=torch.int32, device=dev)
+    S = 48
     po = torch.empty((1, S, n_q, hd), dtype=torch.float32, device=dev)
     pl = torch.empty((1, S, n_q), dtype=torch.float32, device=dev)
     for kc, vc in caches:
         ops.splitkv_decode_merged(q, kc, vc, table, seq_lens, S, hd ** -0.5, po, pl)
     torch.cuda.synchronize()
     return {"copy_bytes": COPY_BYTES, "gemv_bytes": GEMV_BYTES, "gemv_launches": 48,
-            "attn_launches": 12, "attn_splits": S}
+            "read_probe_launches": 24, "attn_launches": 12, "attn_splits": S}
 
 
 def build_model(dev, max_len: int, num_splits: int | None, seed: int = 0):
@@ -179,42 +244,76 @@ def build_model(dev, max_len: int, num_splits: int | None, seed: int = 0):
     return DecodeModel(DecoderConfig(), dev, seed=seed, max_len=max_len, num_splits=num_splits)
 
 
-def run_decode(model, prompt, warmup: int, steps: int):
-    """Feed the prompt, run `warmup` generated steps untimed, time `steps`."""
+def _timed_steps(model, n: int) -> float:
+    """Seconds for n graph replays, HIP events on the replay stream."""
     import torch
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(n):
+        model.step()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) * 1e-3
+
+
+def run_protocol(model, prompt, warmup: int, steps: int):
+    """Feed the prompt, run `warmup` generated steps untimed, time `steps`;
+    returns (seconds per step, tokens, positions timed)."""
     model.reset(prompt)
     for _ in range(prompt.numel() - 1 + warmup):
         model.step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        model.step()
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
+    p0 = prompt.numel() - 1 + warmup
+    dt = _timed_steps(model, steps)
     total = prompt.numel() + warmup + steps
-    return (t1 - t0) / steps, model.state.tokens[0, :total].clone().cpu()
+    return dt / steps, model.state.tokens[0, :total].clone().cpu(), list(range(p0, p0 + steps))
+
+
+def spread_segments(steps: int, lo: int = PROMPT, hi: int = PROMPT + GENERATED - 2):
+    """Up to 4 segments of timed positions covering [lo, hi] evenly: (first
+    position, length) pairs whose lengths sum to `steps`."""
+    n = min(4, steps)
+    lens = [steps // n + (1 if i < steps % n else 0) for i in range(n)]
+    if n == 1:
+        return [(lo + (hi - lo - lens[0] + 1) // 2, lens[0])]
+    span = hi - lo - lens[-1] + 1
+    return [(lo + round(i * span / (n - 1)), lens[i]) for i in range(n)]
+
+
+def run_spread(model, warmup: int, segments):
+    """Time each segment's positions after `warmup` untimed steps before it,
+    on the model's pre-filled KV cache; returns (seconds per step, tokens
+    generated in the timed steps, positions timed)."""
+    total_t, toks, positions = 0.0, [], []
+    for p0, n in segments:
+        model.set_context([p0 - warmup], ids=[1])
+        for _ in range(warmup):
+            model.step()
+        total_t += _timed_steps(model, n)
+        toks.append(model.state.tokens[0, p0 + 1:p0 + n + 1].clone().cpu())
+        positions += list(range(p0, p0 + n))
+    import torch
+    return total_t / len(positions), torch.cat(toks), positions
 
 
 def batch_decode(dev, steps: int = 64, warmup: int = 4, batch: int = 8, seed: int = 5):
     """Config-5 style throughput: `batch` sequences at seeded ragged contexts
     ~U[512, 32768] decoded together through the captured step graph (MFMA
-    GEMM path, split-KV over per-sequence block tables)."""
+    GEMM path, split-KV over per-sequence block tables), over a KV cache
+    filled with seeded random bf16."""
     import torch
     from spark_vllm_ascend_amd.integration.model import DecodeModel, DecoderConfig
     ctx = torch.randint(512, 32768, (batch,), generator=torch.Generator().manual_seed(seed))
     max_len = int(ctx.max()) + warmup + steps + 2
     model = DecodeModel(DecoderConfig(), dev, seed=seed, max_len=max_len, batch=batch)
+    model.fill_kv(seed)
     model.set_context(ctx.tolist())
     model.capture()
     model.set_context(ctx.tolist())
     for _ in range(warmup):
         model.step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        model.step()
-    torch.cuda.synchronize()
-    dt = (time.perf_counter() - t0) / steps
+    dt = _timed_steps(model, steps) / steps
     c = model.cfg
     rb = lambda n, k: n * k // 32 * 18
     weights = c.n_layers * (rb(c.qkv_rows, c.hidden) + rb(c.hidden, c.n_q * c.head_dim)
@@ -232,8 +331,8 @@ def batch_decode(dev, steps: int = 64, warmup: int = 4, batch: int = 8, seed: in
             "plan": {"num_items": model_items, "num_splits": model_splits},
             "bytes_per_step": weights + kv,
             "achieved_gbs": round((weights + kv) / dt / 1e9, 1),
-            "note": "8 sequences, contexts ~U[512, 32768] (seeded), random KV contents, greedy; "
-                    "split-KV over a per-sequence split plan"}
+            "note": "8 sequences, contexts ~U[512, 32768] (seeded), KV cache filled with seeded "
+                    "random bf16, greedy; split-KV over a per-sequence split plan"}
 
 
 def step_bytes(cfg, ctx: int) -> int:
@@ -246,14 +345,27 @@ def step_bytes(cfg, ctx: int) -> int:
     return c.n_layers * (layer + kv + norms) + rb(c.vocab, c.hidden) + c.hidden * 2 * 2
 
 
-def cpu_baseline(model, ctx: int, max_steps: int, budget_s: float):
+def _median_time(fn, reps: int, warm: int = 3) -> float:
+    for _ in range(warm):
+        fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
+
+
+def cpu_baseline(model, ctx: int, reps: int, budget_s: float):
     """The reference's CPU path on this host: bf16 weights (RNE(d*q), the
-    bytes the reference deploys) + F.linear, timed per decode step."""
+    bytes the reference deploys) + F.linear, timed per decode step on all
+    cores and on 4 threads; plus the single-GEMV and attention legs."""
+    import numpy as np
     import torch
     from oracle.cpu_path import CpuDecoder
-    from spark_vllm_ascend_amd.integration.weights import dequantize_bf16
+    from oracle import q4_0 as oq
+    from spark_vllm_ascend_amd.integration.weights import dequantize_bf16, synthetic_q4_0
     cores = len(os.sched_getaffinity(0))
-    torch.set_num_threads(cores)
     c = model.cfg
     layers = []
     for L in model.layers:
@@ -265,19 +377,59 @@ def cpu_baseline(model, ctx: int, max_steps: int, budget_s: float):
             "input_norm": L.input_norm.cpu(), "post_norm": L.post_norm.cpu(),
             "q_norm": L.q_norm.cpu(), "k_norm": L.k_norm.cpu()})
     dec = CpuDecoder(c, layers, model.final_norm.cpu(), model.head.weight.cpu(),
-                     model.cos_sin.cpu(), ctx + max_steps + 1)
+                     model.cos_sin.cpu(), ctx + 2 * reps + 8)
     dec.fill_cache(ctx)
-    dec.step(1, ctx)  # warm-up (first-touch, thread pool)
-    times = []
-    t_start = time.perf_counter()
-    tok = 1
-    for i in range(max_steps):
-        t0 = time.perf_counter()
-        tok = dec.step(tok, ctx + 1 + i)
-        times.append(time.perf_counter() - t0)
-        if time.perf_counter() - t_start > budget_s and len(times) >= 3:
-            break
-    med = statistics.median(times)
+
+    def steps_at(threads: int):
+        torch.set_num_threads(threads)
+        dec.step(1, ctx)  # warm-up (first touch, thread pool)
+        times, tok, t_start = [], 1, time.perf_counter()
+        for i in range(reps):
+            t0 = time.perf_counter()
+            tok = dec.step(tok, ctx + 1 + i)
+            times.append(time.perf_counter() - t0)
+            if time.perf_counter() - t_start > budget_s and len(times) >= 5:
+                break
+        return statistics.median(times), len(times)
+
+    med_all, n_all = steps_at(cores)
+    log(f"  decode step, {cores} threads: {med_all * 1e3:.1f} ms (median of {n_all})")
+    med_4, n_4 = steps_at(4)
+    log(f"  decode step, 4 threads: {med_4 * 1e3:.1f} ms (median of {n_4})")
+
+    # config 1: the single GEMV on pre-dequantised bf16 weights (F.linear),
+    # and the fp32/fp64-accumulating restatement the oracle uses
+    blocks = synthetic_q4_0(GEMV_N, GEMV_K, 500, model.device)
+    w_bf16 = dequantize_bf16(blocks, GEMV_N, GEMV_K).cpu()
+    x = torch.randn((1, GEMV_K)).to(torch.bfloat16)
+    legs = {}
+    for threads in (cores, 4):
+        torch.set_num_threads(threads)
+        t = _median_time(lambda: torch.nn.functional.linear(x, w_bf16), max(reps, 20))
+        legs[f"gemv_9728x2560_f_linear_bf16_{threads}t"] = {
+            "us": round(t * 1e6, 1), "gbs_of_q4_0_bytes": round(GEMV_BYTES / t / 1e9, 2)}
+    blocks_np = blocks.cpu().numpy()
+    x_bits = x.view(torch.int16).numpy().view(np.uint16).reshape(-1)
+    t = _median_time(lambda: oq.gemv_f64(x_bits, blocks_np, GEMV_N, GEMV_K), max(reps, 20), 1)
+    legs["gemv_9728x2560_oracle_c_f64"] = {"us": round(t * 1e6, 1),
+                                           "gbs_of_q4_0_bytes": round(GEMV_BYTES / t / 1e9, 2)}
+    # config 2: fp32 attention at 6144 over a gathered cache (one q head per kv
+    # head group, softmax(q K^T s) V)
+    n_q, n_kv, hd, L = 32, 8, 128, 6144
+    q = torch.randn((n_q, hd))
+    kk = torch.randn((L, n_kv, hd)).to(torch.bfloat16)
+    vv = torch.randn((L, n_kv, hd)).to(torch.bfloat16)
+
+    def attn():
+        k = kk.float().repeat_interleave(n_q // n_kv, dim=1)
+        v = vv.float().repeat_interleave(n_q // n_kv, dim=1)
+        s = torch.bmm(q.unsqueeze(1), k.permute(1, 2, 0).contiguous()).squeeze(1) * hd ** -0.5
+        return torch.bmm(torch.softmax(s, -1).unsqueeze(1), v.permute(1, 0, 2).contiguous())
+    for threads in (cores, 4):
+        torch.set_num_threads(threads)
+        t = _median_time(attn, max(reps, 20))
+        legs[f"attention_ctx6144_fp32_{threads}t"] = {"us": round(t * 1e6, 1)}
+    torch.set_num_threads(cores)
     cpu_model = ""
     try:
         for line in open("/proc/cpuinfo"):
@@ -286,26 +438,32 @@ def cpu_baseline(model, ctx: int, max_steps: int, budget_s: float):
                 break
     except OSError:
         pass
-    return {"value": round(1.0 / med, 3), "unit": "tok/s", "cores": cores, "kind": "port",
-            "ms_per_token": round(med * 1e3, 2), "cpu": cpu_model,
-            "sample": f"{len(times)} decode steps of the 36-layer model at context {ctx + 1}.."
-                      f"{ctx + len(times)} (KV cache pre-filled with random bf16), torch "
-                      f"{torch.__version__} CPU, bf16 F.linear, {cores} threads, median step"}
+    return {"value": round(1.0 / med_all, 3), "unit": "tok/s", "cores": cores, "kind": "port",
+            "ms_per_token": round(med_all * 1e3, 2), "cpu": cpu_model,
+            "threads_4": {"value": round(1.0 / med_4, 3), "ms_per_token": round(med_4 * 1e3, 2),
+                          "steps": n_4},
+            "legs": legs,
+            "sample": f"median of {n_all} decode steps of the 36-layer model at context "
+                      f"{ctx + 1}.. (KV cache pre-filled with seeded random bf16), torch "
+                      f"{torch.__version__} CPU, bf16 F.linear, {cores} threads; the same on 4 "
+                      f"threads ({n_4} steps); legs: the 9728x2560 GEMV and fp32 attention at "
+                      f"6144, median of >= 20"}
 
 
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=4095)
+    ap.add_argument("--steps", type=int, default=GENERATED - 1)
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--runs", type=int, default=3)
-    ap.add_argument("--prompt-len", type=int, default=2048)
+    ap.add_argument("--prompt-len", type=int, default=PROMPT)
     ap.add_argument("--num-splits", type=int, default=0, help="0 = backend default")
-    ap.add_argument("--phase", choices=["all", "roofline", "decode", "counters", "batch"],
+    ap.add_argument("--phase", choices=["all", "roofline", "decode", "counters", "batch", "cpu"],
                     default="all",
                     help="counters: eager launches for a rocprofv3 --pmc run, no timing")
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--cpu-budget", type=float, default=25.0,
+                    help="seconds per decode-step leg of the CPU baseline")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the decode path has no multi-GPU launch (it would "
@@ -329,11 +487,14 @@ def main() -> int:
     if args.phase in ("all", "roofline"):
         log("GEMV roofline (9728x2560, 24 rotating weight sets)")
         result["roofline"] = gemv_roofline(dev, reps=20)
-        log(f"  {result['roofline']['us_per_launch']} us/launch, "
-            f"{result['roofline']['achieved']} GB/s")
-        log("attention roofline (ctx 6144, 12 rotating KV sets)")
+        r = result["roofline"]
+        log(f"  {r['us_per_launch']} us/launch, {r['achieved']} GB/s; read ceiling "
+            f"{r['ceiling']['us']} us ({r['ceiling_gbs']} GB/s)")
+        log("attention roofline (ctx 2048 / 4096 / 6144, rotating KV sets)")
         result["attention"] = attention_roofline(dev, reps=20)
-        log(f"  best splits {result['attention']['best_splits']}: {result['attention']['us']} us")
+        for ctx, a in result["attention"]["by_ctx"].items():
+            log(f"  ctx {ctx}: best splits {a['best_splits']}: {a['us']} us "
+                f"({a['achieved_gbs']} GB/s, ceiling {a['ceiling_gbs']} GB/s)")
         pmc = ROOT / "profiles" / "q4_0_gemv_9728x2560_traffic.json"
         if pmc.exists():
             result["roofline"]["traffic"] = json.loads(pmc.read_text()).get("traffic_bytes")
@@ -342,27 +503,38 @@ def main() -> int:
             print(json.dumps(result))
             return 0
 
-    max_len = args.prompt_len + args.warmup + args.steps + 1
-    log(f"building the 4B model (max_len {max_len})")
+    protocol = args.steps >= GENERATED - 1 and args.prompt_len == PROMPT
+    max_len = max(CAPACITY, args.prompt_len + args.warmup + args.steps + 1)
+    log(f"building the 4B model (block table {-(-max_len // 128)} pages)")
     model = build_model(dev, max_len, args.num_splits or None)
     model.capture()
-    prompt = torch.randint(0, model.cfg.vocab, (args.prompt_len,),
-                           generator=torch.Generator().manual_seed(1234))
+    c = model.cfg
+    if protocol:
+        prompt = torch.randint(0, c.vocab, (args.prompt_len,),
+                               generator=torch.Generator().manual_seed(1234))
+        how = (f"prompt {args.prompt_len} random ids through the decode graph, TPOT over the "
+               f"{args.steps} tokens after {args.warmup} warmup")
+    else:
+        model.fill_kv(1234)
+        segments = spread_segments(args.steps)
+        how = (f"TPOT over {args.steps} tokens in {len(segments)} segments at positions "
+               f"{', '.join(f'{p}..{p + n - 1}' for p, n in segments)} (each after "
+               f"{args.warmup} untimed tokens) over a seeded random KV cache, spread over the "
+               f"protocol's {PROMPT + 1}..{PROMPT + GENERATED} contexts")
     tpots, token_runs = [], []
     for r in range(args.runs):
-        tpot, toks = run_decode(model, prompt, args.warmup, args.steps)
+        if protocol:
+            tpot, toks, positions = run_protocol(model, prompt, args.warmup, args.steps)
+        else:
+            tpot, toks, positions = run_spread(model, args.warmup, segments)
         tpots.append(tpot)
         token_runs.append(toks)
         log(f"run {r}: TPOT {tpot * 1e3:.4f} ms ({1 / tpot:.1f} tok/s)")
     tpot = statistics.median(tpots)
     deterministic = all(torch.equal(token_runs[0], t) for t in token_runs[1:])
-    gen = token_runs[0][args.prompt_len:]
-    valid = bool(((gen >= 0) & (gen < model.cfg.vocab)).all())
-
-    c = model.cfg
-    ctx_lo = args.prompt_len + args.warmup + 1
-    ctx_hi = args.prompt_len + args.warmup + args.steps
-    mean_bytes = statistics.fmean(step_bytes(c, t) for t in (ctx_lo, ctx_hi))
+    gen = token_runs[0][args.prompt_len:] if protocol else token_runs[0]
+    valid = bool(((gen >= 0) & (gen < c.vocab)).all())
+    mean_bytes = statistics.fmean(step_bytes(c, p + 1) for p in positions)
     bound_ms = mean_bytes / (HBM_PEAK_GBS * 1e9) * 1e3
     out = {
         "metric": "batch-1 decode TPOT ms/token (tok/s) 4B Q4_0; GEMV+attn HBM GB/s vs peak",
@@ -376,13 +548,15 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (random-init weights, seeded random prompt ids)",
+        "data": "synthetic (random-init weights, seeded random prompt ids / KV contents)",
         "config": {"workload": "4B Q4_0 decoder: 36 layers, hidden 2560, 32q/8kv x 128, SwiGLU "
-                               "9728, vocab 151936 Q4_0 head, BF16 paged KV block 128; prompt "
-                               f"{args.prompt_len}, greedy decode, TPOT over {args.steps} tokens "
-                               f"after {args.warmup} warmup, median of {args.runs} runs",
-                   "global_batch": 1, "seq_len": ctx_hi, "parallelism": "single GPU",
-                   "num_splits": model.num_splits},
+                               "9728, vocab 151936 Q4_0 head, BF16 paged KV block 128, block "
+                               f"table {model.state.block_table.shape[1]} pages; greedy decode, "
+                               f"{how}; median of {args.runs} runs",
+                   "global_batch": 1, "seq_len": max(positions) + 1,
+                   "contexts": [min(positions) + 1, max(positions) + 1],
+                   "mean_context": round(statistics.fmean(positions) + 1, 1),
+                   "parallelism": "single GPU", "num_splits": model.num_splits},
         "tpot_ms_runs": [round(t * 1e3, 4) for t in tpots],
         "tokens_deterministic_across_runs": deterministic,
         "tokens_in_vocab": valid,
@@ -398,9 +572,9 @@ def main() -> int:
         log("batched decode (8 ragged sequences)")
         out["batch_decode"] = batch_decode(dev)
         log(f"  {out['batch_decode']['tok_s']} tok/s aggregate")
-    if not args.skip_cpu:
+    if not args.skip_cpu and args.phase in ("all", "cpu", "decode"):
         log("CPU baseline")
-        out["cpu_baseline"] = cpu_baseline(model, ctx=args.prompt_len, max_steps=16,
+        out["cpu_baseline"] = cpu_baseline(model, ctx=PROMPT + GENERATED // 2, reps=21,
                                            budget_s=args.cpu_budget)
         log(f"  {out['cpu_baseline']['ms_per_token']} ms/token on "
             f"{out['cpu_baseline']['cores']} cores")

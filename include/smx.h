@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define SMX_ABI_VERSION 5
+#define SMX_ABI_VERSION 6
 
 /* Return codes besides 0 and hipError_t values. */
 #define SMX_EINVAL 10001      /* an argument failed validation */
@@ -435,6 +435,23 @@ int smx_decode_advance(void* stream, int64_t* next_ids,
                        int32_t block_size, int32_t max_len,
                        const void* embed_table, void* embed_out, int64_t vocab,
                        int64_t hidden);
+
+/*
+ * Streaming-read probe (a measurement instrument, no counterpart in the
+ * reference): reads `bytes` (a multiple of 16) from src once with 16-byte
+ * loads, loads_per_lane (1, 2, 4, 8 or 16) of them per lane all in flight,
+ * and writes one uint32 per wave into sink: the XOR of every 32-bit word
+ * that wave read.  Workgroups of 4 waves; with L = loads_per_lane, wave w
+ * of workgroup b reads the 16-byte words b * 256 * L + i * 256 + 64 * w +
+ * lane (i < L, lane < 64), an index past the end reading the last word.
+ * Its time is the HBM ceiling of any kernel that moves the same bytes in one
+ * launch.
+ * sink_size must equal smx_read_probe_sink_size(bytes, loads_per_lane)
+ * (-1 for invalid arguments).
+ */
+int64_t smx_read_probe_sink_size(int64_t bytes, int32_t loads_per_lane);
+int smx_read_probe(void* stream, const void* src, int64_t bytes, uint32_t* sink,
+                   int64_t sink_size, int32_t loads_per_lane);
 
 #ifdef __cplusplus
 }

@@ -363,6 +363,14 @@ class DecodeModel:
         st.slot_mapping.copy_(st.block_table[:, 0].to(torch.int64) * self.cfg.block_size)
         self.head.embed(st.ids, out=self.x)
 
+    def fill_kv(self, seed: int) -> None:
+        """Seeded N(0, 1) bf16 values in every layer's whole KV cache (K and V
+        planes), generated on the device: a cache with realistic contents
+        for decoding at a given context after set_context()."""
+        g = torch.Generator(device=self.device).manual_seed(seed)
+        for L in self.layers:
+            L.kv_cache.normal_(0.0, 1.0, generator=g)
+
     def set_context(self, lengths, ids=None) -> None:
         """Continue every sequence r at position lengths[r] (the KV cache
         below it is whatever it holds): for timing decode at given contexts."""

@@ -16,7 +16,7 @@ import ctypes
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libsmx.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 SMX_EINVAL = 10001
 SMX_EUNSUPPORTED = 10002
 
@@ -65,11 +65,14 @@ SIGNATURES = {
     "smx_q4_0_add_rmsnorm_gemv_swiglu": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _F32],
     "smx_q4_0_add_rmsnorm_gemv_argmax": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _F32],
     "smx_q4_0_argmax_keys_size": [_I64, _I64],
+    "smx_read_probe_sink_size": [_I64, _I32],
+    "smx_read_probe": [_P, _P, _I64, _P, _I64, _I32],
 }
 
 # return types other than int
 RESTYPES = {"smx_q4_0_argmax_keys_size": ctypes.c_int64,
-            "smx_q4_0_gemm_keys_per_row": ctypes.c_int64}
+            "smx_q4_0_gemm_keys_per_row": ctypes.c_int64,
+            "smx_read_probe_sink_size": ctypes.c_int64}
 
 _lib = None
 

@@ -31,7 +31,8 @@ COMMON = [
     # preloading): no scalar-load round trip before a kernel's first loads
     "-mllvm", "-amdgpu-kernarg-preload-count=16",
 ]
-SOURCES = ["q4_0_gemv.hip", "q4_0_gemm.hip", "splitkv_attention.hip", "small_ops.hip", "abi.cpp"]
+SOURCES = ["q4_0_gemv.hip", "q4_0_gemm.hip", "splitkv_attention.hip", "small_ops.hip",
+           "read_probe.hip", "abi.cpp"]
 
 
 def _compile(src: str) -> Path:

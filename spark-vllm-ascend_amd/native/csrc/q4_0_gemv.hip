@@ -436,7 +436,7 @@ struct GemvShape {
 };
 
 // What the GEMV fuses, as far as the launch shape goes.
-enum { KIND_PLAIN = 0, KIND_NORM_STORE = 1, KIND_NORM_SWIGLU = 2 };
+enum { KIND_PLAIN = 0, KIND_NORM_STORE = 1, KIND_NORM_SWIGLU = 2, KIND_NORM_ARGMAX = 3 };
 
 static GemvShape pick_shape(int n_out, int out_per_group, int ngroups, int kind) {
   // Measured on MI355X, in the decode step and on graph-replayed launches
@@ -482,6 +482,9 @@ static GemvShape pick_shape(int n_out, int out_per_group, int ngroups, int kind)
     }
   }
   if (sh.rg == 4 && sh.np > 2) sh.rg = 2;  // 4 row groups only with 1-2 pair groups (VGPRs)
+  // The norm + argmax variant with two row groups needs more than 256 VGPRs
+  // above 4 pair groups per lane (K > 16384) and would spill: one row group.
+  if (kind == KIND_NORM_ARGMAX && sh.np > 4) sh.rg = 1;
   return sh;
 }
 
@@ -490,7 +493,11 @@ static hipError_t dispatch_rg(hipStream_t s, const GemvArgs& a, const GemvShape&
   if constexpr (NPMAX <= 2) {
     if (sh.rg == 4) return launch_fast<NPMAX, 4, PRO, EPI>(s, a, sh.ks);
   }
-  if (sh.rg >= 2) return launch_fast<NPMAX, 2, PRO, EPI>(s, a, sh.ks);
+  // (not instantiated: the norm + argmax variant with two row groups above 4
+  // pair groups per lane, which spills; pick_shape never selects it)
+  if constexpr (!(PRO && EPI == EPI_ARGMAX && NPMAX > 4)) {
+    if (sh.rg >= 2) return launch_fast<NPMAX, 2, PRO, EPI>(s, a, sh.ks);
+  }
   return launch_fast<NPMAX, 1, PRO, EPI>(s, a, sh.ks);
 }
 
@@ -521,7 +528,7 @@ static bool fast_path(int64_t k, const void* x, const void* w, GemvShape* sh, in
 // Grid size of the streaming kernel for an argmax GEMV (keys written).
 static int64_t argmax_workgroups(int64_t n, int64_t k, const void* x, const void* w) {
   GemvShape sh;
-  if (!fast_path(k, x, w, &sh, n, 8)) return -1;
+  if (!fast_path(k, x, w, &sh, n, 8, KIND_NORM_ARGMAX)) return -1;
   return (n + 8 * sh.rg - 1) / (8 * sh.rg);
 }
 
@@ -532,7 +539,7 @@ static hipError_t gemv_dispatch(hipStream_t s, GemvArgs a, int64_t k, int epi, b
   const int kind = !pro ? KIND_PLAIN
                    : epi == EPI_SWIGLU ? KIND_NORM_SWIGLU
                    : epi == EPI_STORE ? KIND_NORM_STORE
-                                      : KIND_PLAIN;
+                                      : KIND_NORM_ARGMAX;
   if (!fast_path(k, a.x, a.w, &sh, a.n_out, epi == EPI_SWIGLU ? 4 : 8, kind)) {
     if (pro || epi == EPI_ARGMAX) return hipErrorInvalidValue;  // callers check first
     if (epi == EPI_SWIGLU)

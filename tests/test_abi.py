@@ -108,3 +108,22 @@ def test_call_raises_with_message():
     native = pkg("native")
     with pytest.raises(native.SmxError, match="k must be a multiple of 32"):
         native.call("smx_q4_0_gemv", None, 16, 16, 16, 64, 100)
+
+
+def test_argmax_keys_follow_launch_shape():
+    """One key per workgroup: 16 rows per workgroup for the 151936 x 2560 head,
+    8 above K = 16384 (the norm + argmax GEMV takes one row group there, two
+    would need more than 256 VGPRs); -1 for K not a multiple of 64."""
+    lib = pkg("native").load()
+    assert lib.smx_q4_0_argmax_keys_size(151936, 2560) == 151936 // 16
+    assert lib.smx_q4_0_argmax_keys_size(4096, 20480) == 4096 // 8
+    assert lib.smx_q4_0_argmax_keys_size(2056, 32768) == 2056 // 8
+    assert lib.smx_q4_0_argmax_keys_size(1000, 100) == -1
+
+
+def test_read_probe_sizes():
+    lib = pkg("native").load()
+    assert lib.smx_read_probe_sink_size(14_008_320, 8) == 4 * -(-14_008_320 // 32768)
+    assert lib.smx_read_probe_sink_size(100, 8) == -1   # not a multiple of 16
+    assert lib.smx_read_probe_sink_size(4096, 3) == -1  # loads not a power of two <= 16
+    assert lib.smx_read_probe(None, 16, 4096, 16, 2, 1) == pkg("native").SMX_EINVAL  # sink size

@@ -103,8 +103,11 @@ def _argmax_via_keys(ops, dev, x, r, g, blocks, n, k):
     return logits, int(ids.item()), int(nxt.item())
 
 
-@pytest.mark.parametrize("n,k", [(151936, 2560), (1000, 256), (4104, 2560)])
+@pytest.mark.parametrize("n,k", [(151936, 2560), (1000, 256), (4104, 2560),
+                                 (4096, 20480), (2056, 32768)])
 def test_add_rmsnorm_gemv_argmax(ops, dev, n, k):
+    """Head GEMV + argmax keys; K = 20480 and 32768 take 5 and 8 pair groups
+    per lane (one row group per workgroup there)."""
     rng = np.random.default_rng(n)
     blocks = oq.make_blocks(n, k, seed=n)
     x, r, g, h, _ = _norm_inputs(rng, k, True)
