@@ -229,12 +229,15 @@ int smx_qknorm_rope_splitkv_decode_merged(
  *     which no split writes, are set to 0 / -inf here, so pass the same
  *     buffers to the planned attention calls that use this plan.
  * positions / slot_mapping ([num_seqs] int64) may be NULL unless the plan
- * feeds smx_qknorm_rope_splitkv_decode_planned_merged.  num_seqs <= 64.
+ * feeds smx_qknorm_rope_splitkv_decode_planned_merged; when both are given,
+ * every record's word 3 carries bit 31 (SMX_SPLITKV_PLAN_HAS_POSITIONS)
+ * above the split index.  num_seqs <= 64.
  * Counterpart of execute_serial's device-side task list, parts =
  * ceil(length / width) from the live length (src/spark_vllm_ascend/kernels/
  * attention.py:120-128), with the splits balanced across the batch.
  */
 #define SMX_SPLITKV_PLAN_WORDS 64
+#define SMX_SPLITKV_PLAN_HAS_POSITIONS 0x80000000u
 int smx_splitkv_plan(void* stream, const int32_t* seq_lens, const int64_t* positions,
                      const int64_t* slot_mapping, const int32_t* block_table,
                      uint32_t* plan, float* partial_o, float* partial_lse,
@@ -258,8 +261,10 @@ int smx_splitkv_decode_planned_merged(
 
 /*
  * smx_qknorm_rope_splitkv_decode_merged over the splits of a plan; the
- * positions and slots come from the plan (smx_splitkv_plan must have been
- * given them).
+ * positions and slots come from the plan.  A record without
+ * SMX_SPLITKV_PLAN_HAS_POSITIONS (a plan built without positions and
+ * slots) writes nothing to the cache and leaves NaN in its sequence's
+ * output: the kernel cannot apply RoPE or write K/V without them.
  */
 int smx_qknorm_rope_splitkv_decode_planned_merged(
     void* stream, const void* qkv, const void* q_gamma, const void* k_gamma,

@@ -120,6 +120,7 @@ def splitkv_decode(q, k_cache, v_cache, table, length, num_splits, scale, tile=1
 
 PLAN_WORDS = 64   # uint32 words per plan record
 PLAN_PAGE0 = 9    # record words 9..63: pages from the split's first token on
+PLAN_HAS_POSITIONS = 1 << 31  # word 3 flag: the record carries a position and a slot
 PLAN_ALIGN = 128  # split lengths are multiples of this
 
 
@@ -142,10 +143,12 @@ def plan_records(lengths, num_items: int, num_splits: int, table: np.ndarray, bl
                  positions=None, slots=None) -> np.ndarray:
     """The plan's records, [num_items + num_seqs, PLAN_WORDS] uint32: per
     split (numbered sequence by sequence) the sequence, first / end token,
-    split index, length, position and slot (int64 as two little-endian
-    words; 0 and -1 when not given) and the block-table entries from the
-    first token's page on (indices clamped to the table row); past the last
-    split, records with sequence -1 and zeros."""
+    split index (bit 31 set when positions and slots were both given:
+    the record can drive the fused q/k-norm + RoPE + KV-write kernel),
+    length, position and slot (int64 as two little-endian words; 0 and -1
+    when not given) and the block-table entries from the first token's page
+    on (indices clamped to the table row); past the last split, records
+    with sequence -1 and zeros."""
     table = np.asarray(table)
     cap = table.shape[1] * block_size
     _, splits = plan_splits(lengths, num_items, num_splits, cap)
@@ -158,7 +161,8 @@ def plan_records(lengths, num_items: int, num_splits: int, table: np.ndarray, bl
         p = int(positions[r]) if positions is not None else 0
         s = int(slots[r]) if slots is not None else -1
         for j, (tb, te) in enumerate(sp):
-            head = [r, tb, te, j, L, p & 0xFFFFFFFF, (p >> 32) & 0xFFFFFFFF,
+            flag = PLAN_HAS_POSITIONS if positions is not None and slots is not None else 0
+            head = [r, tb, te, j | flag, L, p & 0xFFFFFFFF, (p >> 32) & 0xFFFFFFFF,
                     s & 0xFFFFFFFF, (s >> 32) & 0xFFFFFFFF]
             rec[b, :PLAN_PAGE0] = head
             idx = np.minimum(tb // block_size + np.arange(PLAN_WORDS - PLAN_PAGE0),

@@ -80,7 +80,7 @@ def choose_plan(num_seqs: int, n_kv: int = 8) -> tuple[int, int]:
 _WORKSPACES: dict = {}
 
 
-def _workspace(num_seqs: int, num_splits: int, num_heads: int, head_size: int, device):
+def split_partials(num_seqs: int, num_splits: int, num_heads: int, head_size: int, device):
     """Split partials, allocated once per shape and shared by every layer
     (the reference likewise allocates its workspaces once per compile key,
     src/spark_vllm_ascend/integration/model.py:128-131)."""
@@ -116,8 +116,8 @@ class SplitKVDecodeImpl:
                                         value.reshape(-1, self.num_kv_heads, self.head_size),
                                         k_cache, v_cache, attn_metadata.slot_mapping)
         q = query.reshape(num_seqs, self.num_heads, self.head_size)
-        po, pl = _workspace(num_seqs, attn_metadata.num_splits, self.num_heads, self.head_size,
-                            query.device)
+        po, pl = split_partials(num_seqs, attn_metadata.num_splits, self.num_heads,
+                                self.head_size, query.device)
         out = output.view(num_seqs, self.num_heads, self.head_size) if output is not None else None
         if attn_metadata.plan is not None:
             out = torch_ops.splitkv_decode_planned_merged(
@@ -146,18 +146,24 @@ class SplitKVDecodeBackend:
 
     @staticmethod
     def plan(attn_metadata: SplitKVDecodeMetadata, block_size: int, num_heads: int,
-             head_size: int) -> SplitKVDecodeMetadata:
+             head_size: int, positions: torch.Tensor | None = None) -> SplitKVDecodeMetadata:
         """Per-sequence split plan for this step's metadata (num_items > 0,
         at most 64 sequences), enqueued on the current stream; every layer's
-        forward with this metadata then runs over the plan's splits."""
+        forward with this metadata then runs over the plan's splits.  With
+        `positions` (int64, one per sequence) the records also carry each
+        sequence's position and KV slot (metadata.slot_mapping), which the
+        fused q/k-norm + RoPE + KV-write attention needs; a plan built
+        without them makes that kernel return NaN."""
         if attn_metadata.num_items <= 0:
             raise ValueError("set num_items (choose_plan) before planning")
         num_seqs = attn_metadata.seq_lens.numel()
-        po, pl = _workspace(num_seqs, attn_metadata.num_splits, num_heads, head_size,
+        po, pl = split_partials(num_seqs, attn_metadata.num_splits, num_heads, head_size,
                             attn_metadata.seq_lens.device)
         attn_metadata.plan = torch_ops.splitkv_plan(
             attn_metadata.seq_lens, attn_metadata.block_tables, block_size,
-            attn_metadata.num_items, po, pl, plan=attn_metadata.plan)
+            attn_metadata.num_items, po, pl, positions=positions,
+            slot_mapping=attn_metadata.slot_mapping if positions is not None else None,
+            plan=attn_metadata.plan)
         return attn_metadata
 
     @staticmethod

@@ -13,6 +13,9 @@ under the namespace ``smx``:
   smx::splitkv_decode_attention(q, k_cache, v_cache, block_table, seq_lens,
                                 num_splits, scale) -> out   bf16 [seqs, n_q, hd]
   smx::argmax(logits) -> ids                           int64 [rows]
+  smx::layer_run(x, residual, positions, layer_name) -> (y, residual_out)
+      one decoder layer's decode step over the layers layer_run.install()
+      registered (src/spark_vllm_ascend/integration/model.py:46-82)
 
 register() defines them once per process; calling it again is a no-op.
 """
@@ -77,5 +80,15 @@ def register() -> None:
     def _(logits):
         rows = logits.numel() // logits.shape[-1]
         return logits.new_empty((rows,), dtype=torch.int64)
+
+    @torch.library.custom_op(f"{_NS}::layer_run", mutates_args=())
+    def layer_run(x: torch.Tensor, residual: torch.Tensor, positions: torch.Tensor,
+                  layer_name: str) -> tuple[torch.Tensor, torch.Tensor]:
+        from . import layer_run as lr
+        return lr.layer_run(x, residual, positions, layer_name)
+
+    @layer_run.register_fake
+    def _(x, residual, positions, layer_name):
+        return torch.empty_like(x), torch.empty_like(residual)
 
     _done = True

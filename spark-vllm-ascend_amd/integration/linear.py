@@ -14,7 +14,11 @@ same hook for Q4_0 linears on vLLM's LinearMethodBase contract:
       validates the loaded blocks; the kernels stream GGUF blocks directly,
       so no repack happens.
   apply(layer, x, bias=None) -> [..., N] bf16
-      Q4_0 GEMV per activation row (HIP kernel), bias added after.
+      one HIP launch: the Q4_0 GEMV for one activation row, the MFMA Q4_0
+      GEMM for 2..16 rows (K % 64 == 0); more rows (prefill) go through the
+      bf16 weights the reference's stock path uses (dequantised on the
+      device, then a library GEMM), as Q6HeadMethod defers to the stock
+      method outside its one-row case.  Bias added after.
 
 vLLM is not installed in this image; when it is, the class derives from its
 LinearMethodBase so vLLM's loaders accept it unchanged.
@@ -38,6 +42,10 @@ except Exception:  # noqa: BLE001
 
         def process_weights_after_loading(self, layer):
             return None
+
+
+#: activation rows one MFMA Q4_0 GEMM launch serves (the kernel's m limit)
+GEMM_MAX_ROWS = 16
 
 
 class Q4_0Config:
@@ -91,10 +99,24 @@ class Q4_0LinearMethod(_Base):
         if x.dtype != torch.bfloat16:
             raise ValueError(f"expected bf16 activations, got {x.dtype}")
         rows = x.reshape(-1, k).contiguous()
-        out = torch.empty((rows.shape[0], n), dtype=torch.bfloat16, device=x.device)
+        m = rows.shape[0]
         w = layer.qweight.reshape(-1)
-        for i in range(rows.shape[0]):
-            torch_ops.q4_0_gemv(rows[i], w, n, k, out=out[i])
+        if m == 0:
+            out = torch.empty((0, n), dtype=torch.bfloat16, device=x.device)
+        elif m == 1:
+            out = torch_ops.q4_0_gemv(rows, w, n, k)
+        elif m <= GEMM_MAX_ROWS and k % 64 == 0:
+            if rows.data_ptr() % 16:
+                rows = rows.clone()  # the tile kernel stages 16-byte activation chunks
+            out = torch_ops.q4_0_gemm(rows, w, n, k)
+        elif m <= GEMM_MAX_ROWS:
+            # K % 64 != 0: the GEMV (any K % 32 == 0), one launch per row
+            out = torch.empty((m, n), dtype=torch.bfloat16, device=x.device)
+            for i in range(m):
+                torch_ops.q4_0_gemv(rows[i], w, n, k, out=out[i])
+        else:
+            w_bf16 = torch_ops.q4_0_dequant_bf16(w, n, k)
+            out = torch.nn.functional.linear(rows, w_bf16.view(n, k))
         out = out.reshape(*x.shape[:-1], n)
         if bias is not None:
             out = out + bias

@@ -13,9 +13,16 @@ a non-zero return code.
 from __future__ import annotations
 
 import ctypes
+import hashlib
+import json
+import os
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libsmx.so"
+#: when set, load() requires this validation record (written by
+#: spark-vllm-ascend_amd/native/validate.py after a passing GPU test run) to
+#: vouch for the library about to be loaded
+VALIDATION_ENV = "SMX_VALIDATION_RECORD"
 ABI_VERSION = 6
 SMX_EINVAL = 10001
 SMX_EUNSUPPORTED = 10002
@@ -85,8 +92,43 @@ class SmxError(RuntimeError):
         super().__init__(f"{func} failed with code {code}: {detail}")
 
 
+def library_sha256(path: Path = LIB_PATH) -> str:
+    return hashlib.sha256(Path(path).read_bytes()).hexdigest()
+
+
+def check_validation_record(record_path, lib_path: Path = LIB_PATH) -> str:
+    """Raise RuntimeError unless the JSON validation record at record_path
+    vouches for the library at lib_path: a complete GPU test run of this ABI
+    version with no failure and at least one passed test, and the library's
+    sha256.  Returns the digest.  The reference gates its kernel library the
+    same way (src/spark_vllm_ascend/integration/head.py:22-27: a complete
+    validation record whose library_sha256 matches, before load_library)."""
+    try:
+        rec = json.loads(Path(record_path).read_text())
+    except (OSError, ValueError) as exc:
+        raise RuntimeError(f"validation record {record_path} unreadable: {exc}") from exc
+    res = rec.get("pytest", {}) if isinstance(rec, dict) else {}
+    problems = []
+    if rec.get("complete") is not True:
+        problems.append("not complete")
+    if rec.get("abi_version") != ABI_VERSION:
+        problems.append(f"ABI {rec.get('abi_version')} != {ABI_VERSION}")
+    if res.get("exit") != 0 or res.get("failed", 1) != 0 or res.get("errors", 1) != 0:
+        problems.append("the GPU tests did not all pass")
+    if not res.get("passed", 0) > 0:
+        problems.append("no GPU test passed")
+    digest = library_sha256(lib_path) if Path(lib_path).exists() else None
+    if digest is None or rec.get("library_sha256") != digest:
+        problems.append("library_sha256 does not match the library")
+    if problems:
+        raise RuntimeError(f"validation record {record_path} rejected: " + "; ".join(problems))
+    return digest
+
+
 def load() -> ctypes.CDLL:
-    """Load libsmx.so once (after torch) and declare its signatures."""
+    """Load libsmx.so once (after torch) and declare its signatures.  With
+    SMX_VALIDATION_RECORD set, the record must vouch for the library first
+    (check_validation_record)."""
     global _lib
     if _lib is not None:
         return _lib
@@ -98,6 +140,9 @@ def load() -> ctypes.CDLL:
         raise RuntimeError(
             f"{LIB_PATH} is not built; run __graft_entry__.build() or "
             "python spark-vllm-ascend_amd/native/build.py")
+    record = os.environ.get(VALIDATION_ENV)
+    if record:
+        check_validation_record(record, LIB_PATH)
     lib = ctypes.CDLL(str(LIB_PATH))
     for name, argtypes in SIGNATURES.items():
         fn = getattr(lib, name)

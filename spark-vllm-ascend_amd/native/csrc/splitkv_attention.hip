@@ -45,12 +45,16 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 //
 // Plan records (PLAN_WORDS uint32 words each, written by
 // splitkv_plan_kernel): word 0 the sequence (-1: unused record), 1 / 2 the
-// first / end token, 3 the split index within the sequence, 4 the sequence
-// length, 5-6 the position and 7-8 the slot (int64, little-endian), and
-// words PLAN_PAGE0..63 the block-table entries from the first token's page on.
+// first / end token, 3 the split index within the sequence (bit 31 set when
+// the plan was given positions and slots: only such a record can drive the
+// fused q/k-norm + RoPE + KV write, which poisons its output with NaN and
+// writes nothing to the cache otherwise), 4 the sequence length, 5-6 the
+// position and 7-8 the slot (int64, little-endian), and words
+// PLAN_PAGE0..63 the block-table entries from the first token's page on.
 constexpr int PLAN_WORDS = 64;
 constexpr int PLAN_PAGE0 = 9;
 constexpr int PLAN_ALIGN = 128;  // split lengths are multiples of this (4 waves x 32 tokens)
+constexpr uint32_t PLAN_HAS_POSITIONS = 0x80000000u;  // word 3 flag
 
 struct SplitKVArgs {
   const uint16_t* q;  // [num_seqs, n_q, HD] (plain) or the raw QKV row (FUSEQ)
@@ -160,13 +164,16 @@ void splitkv_decode_kernel(
   constexpr int LEN_LANE = PLAN ? 4 : 0, POS_LANE = PLAN ? 5 : 3, SLOT_LANE = PLAN ? 7 : 5;
   uint32_t gv;
   int seq, split, s0, s_end, wlen, w0, pg0;
+  bool pos_ok = true;  // FUSEQ: a position and a slot come with the split
   if constexpr (PLAN) {
     gv = reinterpret_cast<const uint32_t*>(lens_)[(int64_t)blockIdx.y * PLAN_WORDS + lane];
     seq = __builtin_amdgcn_readlane((int)gv, 0);
     if (seq < 0) return;  // an unused record: the plan cleared the unused partials
     s0 = __builtin_amdgcn_readlane((int)gv, 1);
     s_end = __builtin_amdgcn_readlane((int)gv, 2);
-    split = __builtin_amdgcn_readlane((int)gv, 3);
+    const uint32_t w3 = (uint32_t)__builtin_amdgcn_readlane((int)gv, 3);
+    split = (int)(w3 & ~PLAN_HAS_POSITIONS);
+    pos_ok = (w3 & PLAN_HAS_POSITIONS) != 0;
     wlen = ((s_end - s0 + WAVES - 1) / WAVES + TILE - 1) / TILE * TILE;
     w0 = min(s0 + wave * wlen, s_end);
     pg0 = s0 >> bs_log2;
@@ -316,7 +323,7 @@ void splitkv_decode_kernel(
   int64_t slot = -1;
   u32x4 qv = u32x4{0u, 0u, 0u, 0u};
   if constexpr (FUSEQ) {
-    owner = pos >= s0 && pos < s1;
+    owner = pos_ok && pos >= s0 && pos < s1;
     const int64_t pc = pos < 0 ? 0 : (pos >= A.max_position ? A.max_position - 1 : pos);
     c = bf16_bits_to_f32(A.cos_sin[pc * HD + lane]);
     sn = bf16_bits_to_f32(A.cos_sin[pc * HD + 64 + lane]);
@@ -485,7 +492,7 @@ void splitkv_decode_kernel(
       *reinterpret_cast<f32x4*>(dst + 4) = f32x4{acc[4][r], acc[5][r], acc[6][r], acc[7][r]};
     }
   }
-  if (lane == 0) bad_w[wave] = bad_page ? 1 : 0;
+  if (lane == 0) bad_w[wave] = bad_page || (FUSEQ && !pos_ok) ? 1 : 0;
   if (lane < G) {
     l_w[wave][lane] = l_tot;
     m_w[wave][lane] = m_mine;  // lane h keeps head h
@@ -548,8 +555,17 @@ __global__ __launch_bounds__(64 * MERGE_WAVES) void lse_merge_kernel(
     uint16_t* __restrict__ out, int num_splits, int n_q, int nw) {
   __shared__ float m_s[MERGE_WAVES], l_s[MERGE_WAVES], a_s[MERGE_WAVES][64];
   __shared__ int bad_s[MERGE_WAVES];
-  const int h = blockIdx.x >> 1, seq = blockIdx.y;
-  const int lane = threadIdx.x & 63, d = (blockIdx.x & 1) * 64 + lane;
+  // Workgroup b serves kv head b % n_kv (its 2 G head halves are b / n_kv):
+  // workgroups go to the XCDs round-robin by linear id, and the attention
+  // kernel's workgroups of kv head j (kv heads fastest) run on XCD j % 8, so
+  // with n_kv = 8 a head's partials are read on the XCD whose L2 wrote them.
+  // (n_q not a multiple of G: workgroup b serves head b / 2, half b % 2.)
+  const int n_kv = n_q % G == 0 ? n_q / G : n_q;
+  const int kvh = blockIdx.x % n_kv, j = blockIdx.x / n_kv;
+  const int h = n_q % G == 0 ? kvh * G + (j >> 1) : (int)blockIdx.x >> 1;
+  const int half = n_q % G == 0 ? (j & 1) : (int)blockIdx.x & 1;
+  const int seq = blockIdx.y;
+  const int lane = threadIdx.x & 63, d = half * 64 + lane;
   const int v = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t row = (int64_t)seq * num_splits * n_q + h;  // (seq, split 0, h)
   const int cnt = v < num_splits ? (num_splits - 1 - v) / nw + 1 : 0;  // this wave's splits
@@ -670,7 +686,8 @@ __global__ __launch_bounds__(64) void splitkv_plan_kernel(
       const int tb = j * chunk, te = min(tb + chunk, li);
       const int64_t p = positions ? positions[i] : 0;
       const int64_t sl = slot_mapping ? slot_mapping[i] : -1;
-      const uint32_t head[PLAN_PAGE0] = {(uint32_t)i, (uint32_t)tb, (uint32_t)te, (uint32_t)j,
+      const uint32_t flag = positions && slot_mapping ? PLAN_HAS_POSITIONS : 0u;
+      const uint32_t head[PLAN_PAGE0] = {(uint32_t)i, (uint32_t)tb, (uint32_t)te, (uint32_t)j | flag,
                                          (uint32_t)li, (uint32_t)p, (uint32_t)(p >> 32),
                                          (uint32_t)sl, (uint32_t)(sl >> 32)};
       if (lane < PLAN_PAGE0) {

@@ -277,3 +277,32 @@ def test_fused_planned(ops, dev, lengths, bs, items, splits):
         ref = oatt.attention_f64(qf[i], k, v, HD ** -0.5)
         got = f32_of(out).reshape(ns, N_Q, HD)[i]
         assert np.abs(got - ref).max() < 2e-2, f"seq {i} (L={L})"
+
+
+@pytest.mark.parametrize("given", ["none", "positions_only"])
+def test_fused_planned_without_positions_poisons(ops, dev, given):
+    """A plan built without positions and slots cannot drive the fused
+    q/k-norm + RoPE + KV-write kernel: every sequence's output is NaN and the
+    caches are left as they were (no K/V written at a made-up slot)."""
+    import torch
+    lengths, bs, items, splits = [300, 4096, 1], 128, 24, 8
+    rng = np.random.default_rng(77)
+    c = _fused_case(rng, lengths, bs, dev)
+    kc, vc = c["kc"].clone(), c["vc"].clone()
+    ns = len(lengths)
+    po = torch.empty((ns, splits, N_Q, HD), dtype=torch.float32, device=dev)
+    pl = torch.empty((ns, splits, N_Q), dtype=torch.float32, device=dev)
+    kw = {} if given == "none" else {"positions": c["pos"]}
+    plan = ops.splitkv_plan(c["sl"], c["table"], bs, items, po, pl, **kw)
+    rec = plan.cpu().numpy().view(np.uint32)
+    ref = oatt.plan_records(lengths, items, splits, c["np"]["table"], bs,
+                            positions=c["np"]["pos"] if kw else None)
+    np.testing.assert_array_equal(rec, ref)
+    assert not (rec[:, 3] & oatt.PLAN_HAS_POSITIONS).any()
+    out = ops.qknorm_rope_splitkv_decode_planned_merged(c["qkv"], c["qg"], c["kg"], c["cs"], kc,
+                                                        vc, c["table"], plan, items, HD ** -0.5,
+                                                        EPS, N_Q, po, pl)
+    torch.cuda.synchronize()
+    assert np.isnan(f32_of(out)).all()
+    np.testing.assert_array_equal(bits_of(kc), bits_of(c["kc"]))
+    np.testing.assert_array_equal(bits_of(vc), bits_of(c["vc"]))

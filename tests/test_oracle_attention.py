@@ -119,16 +119,22 @@ def test_plan_records_layout():
     rec = oatt.plan_records([300, 0, 8000], 4, 8, table, 128, positions=[299, -1, 7999],
                             slots=[5, -1, 1 << 33])
     # chunk = 128 * ceil(max(ceil(8300 / 4), ceil(8000 / 8)) / 128) = 2176
+    F = oatt.PLAN_HAS_POSITIONS  # word 3 flag: positions and slots were given
     assert rec.shape == (7, oatt.PLAN_WORDS)
-    assert rec[0, :5].tolist() == [0, 0, 300, 0, 300]
+    assert rec[0, :5].tolist() == [0, 0, 300, F, 300]
     assert rec[0, 5:9].tolist() == [299, 0, 5, 0]
     assert rec[0, 9:12].tolist() == [0, 1, 2]
-    assert rec[1, :5].tolist() == [2, 0, 2176, 0, 8000]
+    assert rec[1, :5].tolist() == [2, 0, 2176, F, 8000]
     assert rec[1, 7:9].tolist() == [0, 2]                  # slot 2^33
-    assert rec[4, :5].tolist() == [2, 6528, 8000, 3, 8000]
+    assert rec[4, :5].tolist() == [2, 6528, 8000, 3 | F, 8000]
     assert rec[4, 9] == 140 + 6528 // 128                   # page of token 6528
     assert rec[4, -1] == 140 + 69                           # clamped to the row's end
     assert rec[5, 0] == 0xFFFFFFFF and not rec[5, 1:].any()  # unused
+    # without positions (or without slots) no record carries the flag
+    for kw in ({}, {"positions": [299, -1, 7999]}, {"slots": [5, -1, 1 << 33]}):
+        bare = oatt.plan_records([300, 0, 8000], 4, 8, table, 128, **kw)
+        assert bare[0, 3] == 0 and bare[4, 3] == 3
+        assert bare[0, 5:7].tolist() == ([299, 0] if "positions" in kw else [0, 0])
 
 
 @pytest.mark.parametrize("lengths,items,splits", [([700, 33, 1], 6, 4), ([2000, 500], 3, 8)])

@@ -55,6 +55,11 @@ def test_fake_shapes():
         assert out.shape == (1, 32, 128)
         ids = torch.ops.smx.argmax(torch.empty((3, 1000), dtype=torch.bfloat16))
         assert ids.shape == (3,) and ids.dtype == torch.int64
+        # the reference's per-layer seam: (y, residual) shaped like its inputs
+        # (src/spark_vllm_ascend/integration/model.py:81-82)
+        y, r = torch.ops.smx.layer_run(x, x, torch.empty(1, dtype=torch.int64),
+                                       "model.layers.0.self_attn.attn")
+        assert y.shape == r.shape == (1, 2560) and y.dtype == r.dtype == torch.bfloat16
 
 
 @pytest.mark.gpu

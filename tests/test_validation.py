@@ -1,0 +1,88 @@
+"""The validation-gated load of libsmx.so (CPU): native.load() refuses the
+library unless the record named by SMX_VALIDATION_RECORD vouches for it --
+complete, this ABI version, a GPU test run without failures, the library's
+sha256 -- as the reference refuses its kernel library without a complete
+validation record whose digest matches (src/spark_vllm_ascend/integration/
+head.py:22-27)."""
+import json
+import os
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+
+from _util import pkg
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def _record(tmp_path, **over):
+    native = pkg("native")
+    validate = pkg("native.validate")
+    rec = validate.make_record(0, {"passed": 350, "failed": 0, "errors": 0, "skipped": 6},
+                               native.LIB_PATH)
+    for k, v in over.items():
+        if k.startswith("pytest_"):
+            rec["pytest"][k[7:]] = v
+        else:
+            rec[k] = v
+    path = tmp_path / "validation.json"
+    path.write_text(json.dumps(rec))
+    return path
+
+
+def test_record_for_this_library_is_accepted(tmp_path):
+    native = pkg("native")
+    path = _record(tmp_path)
+    assert native.check_validation_record(path) == native.library_sha256()
+    assert json.loads(path.read_text())["abi_version"] == native.ABI_VERSION
+
+
+@pytest.mark.parametrize("over,why", [
+    ({"complete": False}, "not complete"),
+    ({"abi_version": 1}, "ABI"),
+    ({"library_sha256": "0" * 64}, "sha256"),
+    ({"pytest_exit": 1}, "did not all pass"),
+    ({"pytest_failed": 2}, "did not all pass"),
+    ({"pytest_errors": 1}, "did not all pass"),
+    ({"pytest_passed": 0}, "no GPU test passed"),
+])
+def test_bad_records_are_rejected(tmp_path, over, why):
+    native = pkg("native")
+    with pytest.raises(RuntimeError, match=why):
+        native.check_validation_record(_record(tmp_path, **over))
+
+
+def test_missing_or_garbled_record(tmp_path):
+    native = pkg("native")
+    with pytest.raises(RuntimeError, match="unreadable"):
+        native.check_validation_record(tmp_path / "absent.json")
+    bad = tmp_path / "bad.json"
+    bad.write_text("{not json")
+    with pytest.raises(RuntimeError, match="unreadable"):
+        native.check_validation_record(bad)
+
+
+def test_record_of_another_library_is_rejected(tmp_path):
+    native = pkg("native")
+    other = tmp_path / "libsmx.so"
+    other.write_bytes(native.LIB_PATH.read_bytes() + b"\0")
+    with pytest.raises(RuntimeError, match="sha256"):
+        native.check_validation_record(_record(tmp_path), other)
+
+
+@pytest.mark.parametrize("good", [True, False])
+def test_load_is_gated_by_the_environment(tmp_path, good):
+    """In a fresh process (load() caches the library): with the variable set,
+    load() succeeds only when the record vouches for the library."""
+    path = _record(tmp_path, **({} if good else {"library_sha256": "f" * 64}))
+    code = ("import __graft_entry__ as g; g.load_package(); "
+            "import spark_vllm_ascend_amd.native as n; n.load(); print('loaded')")
+    env = dict(os.environ, SMX_VALIDATION_RECORD=str(path))
+    res = subprocess.run([sys.executable, "-c", code], cwd=ROOT, env=env, capture_output=True,
+                         text=True, timeout=300)
+    if good:
+        assert res.returncode == 0 and "loaded" in res.stdout, res.stderr
+    else:
+        assert res.returncode != 0 and "rejected" in res.stderr
