@@ -335,6 +335,71 @@ def batch_decode(dev, steps: int = 64, warmup: int = 4, batch: int = 8, seed: in
                     "random bf16, greedy; split-KV over a per-sequence split plan"}
 
 
+def step_breakdown(model, ctx: int, reps: int = 10):
+    """Unprofiled per-kernel times of one decode step at context ctx: each
+    kernel class of a layer timed alone in a captured graph of its 36
+    launches (one per layer, so every launch streams that layer's own
+    weights and KV cache, beyond the 256 MB Infinity Cache), the head as the
+    difference between a graph of the 36 gate/up launches with and without
+    it.  Per-launch times include the gap to the next launch, as in the
+    step, so their per-step sum can be set against the measured TPOT
+    (rocprofv3's kernel trace inflates every dispatch)."""
+    import torch
+    from spark_vllm_ascend_amd.native import torch_ops as ops
+    c, st, L = model.cfg, model.state, model.layers
+    n = len(L)
+    model.set_context([ctx - 1], ids=[1])
+    keys = model.argmax_keys.view(-1)
+    kernels = {
+        "qkv": ("add+RMSNorm + QKV GEMV 6144x2560", lambda i: ops.add_rmsnorm_gemv(
+            model.d, model.res_b, L[i].input_norm, L[i].qkv.qweight, c.qkv_rows, c.hidden, c.eps,
+            residual_out=model.res_a, out=model.qkv_out)),
+        "attention": ("q/k norm + RoPE + KV write + split-KV decode, then the LSE merge "
+                      "(two launches)", lambda i: ops.qknorm_rope_splitkv_decode_merged(
+            model.qkv_out, L[i].q_norm, L[i].k_norm, model.cos_sin, st.positions, st.slot_mapping,
+            L[i].kv_cache[0], L[i].kv_cache[1], st.block_table, st.seq_lens, model.num_splits,
+            model.scale, c.eps, c.n_q, model.partial_o, model.partial_lse, out=model.attn)),
+        "o_proj": ("o_proj GEMV 2560x4096", lambda i: ops.q4_0_gemv(
+            model.attn, L[i].o_proj.qweight, c.hidden, c.n_q * c.head_dim, out=model.o)),
+        "gate_up": ("add+RMSNorm + gate/up GEMV 19456x2560 + SwiGLU", lambda i: ops.add_rmsnorm_gemv_swiglu(
+            model.o, model.res_a, L[i].post_norm, L[i].gate_up.qweight, c.intermediate, c.hidden,
+            c.eps, residual_out=model.res_b, out=model.act)),
+        "down": ("down GEMV 2560x9728", lambda i: ops.q4_0_gemv(
+            model.act, L[i].down.qweight, c.hidden, c.intermediate, out=model.d)),
+    }
+    out = {}
+    for key, (what, f) in kernels.items():
+        us = time_graph(lambda: [f(i) for i in range(n)], n, reps)
+        out[key] = {"what": what, "us_per_layer": round(us, 3)}
+    gu = kernels["gate_up"][1]
+
+    def head():
+        ops.add_rmsnorm_gemv_argmax(model.d, model.res_b, model.final_norm, model.head.q4_0_head,
+                                    c.vocab, c.hidden, c.eps, keys, out=model.logits)
+
+    def advance():
+        ops.decode_advance(st.next_ids, st.ids, st.positions, st.seq_lens, st.slot_mapping,
+                           st.block_table, c.block_size, tokens_out=st.tokens,
+                           forced_ids=st.forced, forced_len=st.forced_len,
+                           argmax_keys=model.argmax_keys, embed_table=model.head.weight,
+                           embed_out=model.x)
+    base = time_graph(lambda: [gu(i) for i in range(n)], n, reps) * n
+    with_head = time_graph(lambda: ([gu(i) for i in range(n)], head()), n + 1, reps) * (n + 1)
+    out["head"] = {"what": "final add+RMSNorm + Q4_0 head GEMV 151936x2560 + argmax keys",
+                   "us_per_step": round(with_head - base, 3)}
+    with_adv = time_graph(lambda: ([gu(i) for i in range(n)], advance()), n + 1, reps) * (n + 1)
+    out["advance"] = {"what": "argmax reduction, step advance, next embedding row",
+                      "us_per_step": round(with_adv - base, 3)}
+    per_layer = sum(v["us_per_layer"] for v in out.values() if "us_per_layer" in v)
+    total = n * per_layer + out["head"]["us_per_step"] + out["advance"]["us_per_step"]
+    model.set_context([ctx - 1], ids=[1])
+    return {"context": ctx, "kernels": out, "us_per_layer": round(per_layer, 3),
+            "per_step_sum_ms": round(total / 1e3, 4),
+            "timing": "HIP events over captured graphs of each kernel class's 36 launches (each "
+                      "layer's own weights / KV cache), per-launch mean including the gap to "
+                      "the next launch; the head and the advance kernel by difference"}
+
+
 def step_bytes(cfg, ctx: int) -> int:
     c = cfg
     rb = lambda n, k: n * k // 32 * 18
@@ -462,6 +527,8 @@ def main() -> int:
                     default="all",
                     help="counters: eager launches for a rocprofv3 --pmc run, no timing")
     ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--skip-breakdown", action="store_true",
+                    help="no per-kernel step breakdown (e.g. under a profiler)")
     ap.add_argument("--cpu-budget", type=float, default=25.0,
                     help="seconds per decode-step leg of the CPU baseline")
     args = ap.parse_args()
@@ -568,6 +635,13 @@ def main() -> int:
                                         "shape), README.en.md:87; not this exact workload"},
     }
     out.update(result)
+    if not args.skip_breakdown:
+        log("step breakdown (each kernel class alone, at the timed steps' mean context)")
+        out["step_breakdown"] = step_breakdown(model, int(round(statistics.fmean(positions))) + 1)
+        sb = out["step_breakdown"]
+        sb["measured_ms"] = round(tpot * 1e3, 4)
+        log(f"  per layer {sb['us_per_layer']} us; per step {sb['per_step_sum_ms']} ms "
+            f"(measured {tpot * 1e3:.4f} ms)")
     if args.phase == "all":
         log("batched decode (8 ragged sequences)")
         out["batch_decode"] = batch_decode(dev)
