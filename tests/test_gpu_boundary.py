@@ -10,7 +10,9 @@
     model's own step (logits within bf16 tolerance, greedy tokens equal
     except near-ties) and the float64 oracle; several sequences, bit for bit
     against the decode model's batched step (the same kernels in the same
-    order); a full-size layer at context 4096 against the oracle layer.
+    order); the chain captured once in a CUDA graph and replayed at every
+    position, bit for bit against the eager chain; a full-size layer at
+    context 4096 against the oracle layer.
 """
 import numpy as np
 import pytest
@@ -195,6 +197,81 @@ def test_layer_run_batched_bitwise_against_batched_step(dev):
                              rtol=1e-2, atol_frac=1e-2, what=f"logits at {pos}")
         for La, Lb in zip(a.layers, b.layers):
             np.testing.assert_array_equal(bits_of(Lb.kv_cache), bits_of(La.kv_cache))
+    finally:
+        lr.uninstall()
+
+
+def test_layer_run_chain_replays_in_a_graph(dev):
+    """The seam is graph-safe, as the reference's op is: the model loop over
+    torch.ops.smx.layer_run captured once in a CUDA graph, replayed at every
+    position with the step's positions / lengths / slots updated in place
+    (and the captured chain reading the new embedding row), equals the eager
+    chain bit for bit -- normalised output, logits and the KV cache."""
+    import torch
+    m = pkg("integration.model")
+    pkg("integration.custom_ops").register()
+    ops = pkg("native.torch_ops")
+    lr = pkg("integration.layer_run")
+    T = 12
+    seq = np.random.default_rng(29).integers(0, 1000, T).tolist()
+
+    # eager reference: model e, every position
+    e = m.DecodeModel(_tiny_cfg(), dev, seed=29, max_len=64, num_splits=2)
+    lr.uninstall()
+    lr.install(e)
+    want_y, want_logits = [], []
+    try:
+        for pos, tok in enumerate(seq):
+            md, p = _metadata(e, [pos])
+            y, logits = _chain(e, [tok], p, md)
+            want_y.append(bits_of(y))
+            want_logits.append(bits_of(logits))
+        want_kv = [bits_of(L.kv_cache) for L in e.layers]
+    finally:
+        lr.uninstall()
+    del e
+
+    # the same chain captured once over static inputs: model g
+    g = m.DecodeModel(_tiny_cfg(), dev, seed=29, max_len=64, num_splits=2)
+    c, bs = g.cfg, g.cfg.block_size
+    lr.install(g)
+    try:
+        md, pos_t = _metadata(g, [0])
+        emb = torch.empty((1, c.hidden), dtype=torch.bfloat16, device=dev)
+        lr.set_attention_metadata(md)
+
+        def chain():
+            y, r = ops.add_rmsnorm(emb, None, g.layers[0].input_norm, c.eps)
+            for L in g.layers:
+                y, r = torch.ops.smx.layer_run(y, r, pos_t, L.name)
+            return y, ops.q4_0_gemv(y, g.head.q4_0_head, c.vocab, c.hidden)
+
+        def set_step(pos, tok):
+            emb.copy_(g.head.embed(torch.tensor([tok], dtype=torch.int64, device=dev)))
+            pos_t.fill_(pos)
+            md.seq_lens.fill_(pos + 1)
+            md.slot_mapping.fill_(int(g.state.block_table[0, pos // bs]) * bs + pos % bs)
+
+        # warm-up outside the graph writes position 0 once; the replays
+        # below rewrite it with the same values
+        set_step(0, seq[0])
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            chain()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            y_s, logits_s = chain()
+        for pos, tok in enumerate(seq):
+            set_step(pos, tok)
+            graph.replay()
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(bits_of(y_s), want_y[pos], err_msg=f"y at {pos}")
+            np.testing.assert_array_equal(bits_of(logits_s), want_logits[pos],
+                                          err_msg=f"logits at {pos}")
+        for L, kv in zip(g.layers, want_kv):
+            np.testing.assert_array_equal(bits_of(L.kv_cache), kv)
     finally:
         lr.uninstall()
 
