@@ -318,11 +318,80 @@ def run_spread(model, warmup: int, segments):
     return total_t / len(positions), torch.cat(toks), positions
 
 
-def batch_decode(dev, steps: int = 64, warmup: int = 4, batch: int = 8, seed: int = 5):
+def batch_breakdown(model, ctx, reps: int = 10):
+    """Unprofiled per-class times of the batched step, as step_breakdown does
+    for one sequence: each kernel class of a layer in a captured graph of its
+    36 launches (each layer's own weights and KV cache), per-launch means
+    including the gap to the next launch; the head (final add+RMSNorm + head
+    GEMM with argmax keys) and the advance kernel by difference against the
+    36 gate/up launches.  Resets the contexts first, and leaves the model's
+    state advanced."""
+    from spark_vllm_ascend_amd.native import torch_ops as ops
+    m, c, st, L = model, model.cfg, model.state, model.layers
+    n, B = len(L), model.batch
+    m.set_context(list(ctx))
+    ops.splitkv_plan(st.seq_lens, st.block_table, c.block_size, m.num_items, m.partial_o,
+                     m.partial_lse, positions=st.positions, slot_mapping=st.slot_mapping,
+                     plan=m.plan)
+    kernels = {
+        "norm_in": ("residual add + input RMSNorm, B rows", 1, lambda i: ops.add_rmsnorm(
+            m.d, m.res_b, L[i].input_norm, c.eps, out=m.h, residual_out=m.res_a)),
+        "qkv": ("QKV GEMM 6144x2560, m = B", 1, lambda i: ops.q4_0_gemm(
+            m.h, L[i].qkv.qweight, c.qkv_rows, c.hidden, out=m.qkv_out)),
+        "attention": ("q/k norm + RoPE + KV write + split-KV over the plan, then the LSE merge "
+                      "(two launches)", 2, lambda i: ops.qknorm_rope_splitkv_decode_planned_merged(
+            m.qkv_out, L[i].q_norm, L[i].k_norm, m.cos_sin, L[i].kv_cache[0], L[i].kv_cache[1],
+            st.block_table, m.plan, m.num_items, m.scale, c.eps, c.n_q, m.partial_o,
+            m.partial_lse, out=m.attn)),
+        "o_proj": ("o_proj GEMM 2560x4096, m = B", 1, lambda i: ops.q4_0_gemm(
+            m.attn.view(B, -1), L[i].o_proj.qweight, c.hidden, c.n_q * c.head_dim, out=m.o)),
+        "norm_post": ("residual add + post-attention RMSNorm, B rows", 1, lambda i: ops.add_rmsnorm(
+            m.o, m.res_a, L[i].post_norm, c.eps, out=m.h2, residual_out=m.res_b)),
+        "gate_up": ("gate/up GEMM 19456x2560 + SwiGLU, m = B", 1, lambda i: ops.q4_0_gemm_swiglu(
+            m.h2, L[i].gate_up.qweight, c.intermediate, c.hidden, out=m.act)),
+        "down": ("down GEMM 2560x9728, m = B", 1, lambda i: ops.q4_0_gemm(
+            m.act, L[i].down.qweight, c.hidden, c.intermediate, out=m.d)),
+    }
+    out = {}
+    for key, (what, launches, f) in kernels.items():
+        us = time_graph(lambda: [f(i) for i in range(n)], n * launches, reps) * launches
+        out[key] = {"what": what, "us_per_layer": round(us, 3)}
+    gu = kernels["gate_up"][2]
+
+    def head():
+        ops.add_rmsnorm(m.d, m.res_b, m.final_norm, c.eps, out=m.h)
+        ops.q4_0_gemm_argmax(m.h, m.head.q4_0_head, c.vocab, c.hidden, m.argmax_keys,
+                             out=m.logits)
+
+    def advance():
+        ops.decode_advance(st.next_ids, st.ids, st.positions, st.seq_lens, st.slot_mapping,
+                           st.block_table, c.block_size, tokens_out=st.tokens,
+                           forced_ids=st.forced, forced_len=st.forced_len,
+                           argmax_keys=m.argmax_keys, embed_table=m.head.weight, embed_out=m.x)
+    base = time_graph(lambda: [gu(i) for i in range(n)], n, reps) * n
+    with_head = time_graph(lambda: ([gu(i) for i in range(n)], head()), n + 2, reps) * (n + 2)
+    out["head"] = {"what": "final add+RMSNorm + Q4_0 head GEMM 151936x2560 + argmax keys",
+                   "us_per_step": round(with_head - base, 3)}
+    m.set_context(list(ctx))
+    with_adv = time_graph(lambda: ([gu(i) for i in range(n)], advance()), n + 1, reps) * (n + 1)
+    out["advance"] = {"what": "argmax reduction, step advance, next embedding rows",
+                      "us_per_step": round(with_adv - base, 3)}
+    per_layer = sum(v["us_per_layer"] for v in out.values() if "us_per_layer" in v)
+    total = n * per_layer + out["head"]["us_per_step"] + out["advance"]["us_per_step"]
+    return {"kernels": out, "us_per_layer": round(per_layer, 3),
+            "per_step_sum_ms": round(total / 1e3, 4),
+            "timing": "HIP events over captured graphs of each kernel class's 36 launches, "
+                      "per-launch mean including the gap to the next launch; the head and the "
+                      "advance kernel by difference; one plan launch per step not included"}
+
+
+def batch_decode(dev, steps: int = 64, warmup: int = 4, batch: int = 8, seed: int = 5,
+                 breakdown: bool = True):
     """Config-5 style throughput: `batch` sequences at seeded ragged contexts
     ~U[512, 32768] decoded together through the captured step graph (MFMA
     GEMM path, split-KV over per-sequence block tables), over a KV cache
-    filled with seeded random bf16."""
+    filled with seeded random bf16; with `breakdown`, the unprofiled
+    per-class times of that step (batch_breakdown)."""
     import torch
     from spark_vllm_ascend_amd.integration.model import DecodeModel, DecoderConfig
     ctx = torch.randint(512, 32768, (batch,), generator=torch.Generator().manual_seed(seed))
@@ -343,9 +412,12 @@ def batch_decode(dev, steps: int = 64, warmup: int = 4, batch: int = 8, seed: in
     mid = ctx.to(torch.float64) + warmup + steps / 2
     kv = int((mid * 2 * c.n_kv * c.head_dim * 2 * c.n_layers).sum())
     model_items, model_splits = model.num_items, model.num_splits
+    bd = batch_breakdown(model, ctx.tolist()) if breakdown else None
     del model
     torch.cuda.empty_cache()
-    return {"batch": batch, "contexts": ctx.tolist(), "steps": steps, "ms_per_step": round(dt * 1e3, 4),
+    extra = {"step_breakdown": bd} if bd else {}
+    return {**extra, "batch": batch, "contexts": ctx.tolist(), "steps": steps,
+            "ms_per_step": round(dt * 1e3, 4),
             "tok_s": round(batch / dt, 2),
             # every sequence advances one token per step: its TPOT is the step time
             "tpot_ms_per_sequence": [round(dt * 1e3, 4)] * batch,
