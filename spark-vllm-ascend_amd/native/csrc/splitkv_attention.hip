@@ -103,7 +103,7 @@ __device__ __forceinline__ void norm_rope_head(float a, float b, float ga, float
 // gives the 4-wave 64-token variant 277 registers, one workgroup per CU);
 // without, the compiler's choice (the one-sequence step measured 1.7% slower
 // with the bound, which moves the MFMA accumulators out of AGPRs).
-template <int WAVES, int BLK, bool FUSEQ, bool PLAN>
+template <int WAVES, int BLK, bool FUSEQ, bool PLAN, bool RECFAST = false>
 __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(PLAN ? 2 : 1)))
 void splitkv_decode_kernel(
     const int32_t* block_table_, const void* lens_, const void* pa_, const void* pb_,
@@ -145,8 +145,11 @@ void splitkv_decode_kernel(
   // round-robin) and the 8 heads of the same tokens -- one 2 KB K row and
   // one V row per token -- are read together.  Measured: 2% off one
   // sequence's decode step against split-fastest; split-slowest made an
-  // 8-sequence step 15% slower.
-  const int kvh = blockIdx.x;
+  // 8-sequence step 15% slower.  RECFAST (plans of 8k records): records
+  // fastest, so the 8 heads of a record share one XCD instead (the launcher
+  // says why).
+  const int kvh = RECFAST ? blockIdx.y : blockIdx.x;
+  const int rec = RECFAST ? blockIdx.x : blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int cap = max_blocks << bs_log2;
@@ -166,7 +169,7 @@ void splitkv_decode_kernel(
   int seq, split, s0, s_end, wlen, w0, pg0;
   bool pos_ok = true;  // FUSEQ: a position and a slot come with the split
   if constexpr (PLAN) {
-    gv = reinterpret_cast<const uint32_t*>(lens_)[(int64_t)blockIdx.y * PLAN_WORDS + lane];
+    gv = reinterpret_cast<const uint32_t*>(lens_)[(int64_t)rec * PLAN_WORDS + lane];
     seq = __builtin_amdgcn_readlane((int)gv, 0);
     if (seq < 0) return;  // an unused record: the plan cleared the unused partials
     s0 = __builtin_amdgcn_readlane((int)gv, 1);
@@ -746,10 +749,24 @@ int launch_splitkv(void* stream, smx::SplitKVArgs a, int32_t num_seqs, int32_t b
     if (n >= 1 && (w == 1 || w == 2 || w == 4 || w == 8)) waves = w;
     if (n == 2 && (b == 32 || b == 64)) blk = b;
   }
-  const dim3 grid = plan ? dim3(a.n_kv, num_records, 1) : dim3(a.n_kv, a.num_splits, num_seqs);
+  // A plan of 8k records runs records fastest: workgroups go to the XCDs
+  // round-robin by linear id (record + records * kv head), so all kv heads of
+  // one record share an XCD and its requests cover whole token rows
+  // (8-sequence step, 96 records: attention 88.6 against 90.8-91.4 µs per
+  // layer, the step 4.597 against 4.675 ms).  Capacity splits keep kv heads
+  // fastest: the merge reads a kv head's partials on that head's XCD.
+  const bool recfast = plan && num_records % 8 == 0;
+  const dim3 grid = plan ? (recfast ? dim3(num_records, a.n_kv, 1) : dim3(a.n_kv, num_records, 1))
+                         : dim3(a.n_kv, a.num_splits, num_seqs);
 #define SMX_ATTN_LAUNCH(W, B)                                                                   \
   do {                                                                                          \
-    if (plan)                                                                                   \
+    if (plan && recfast)                                                                        \
+      hipLaunchKernelGGL((smx::splitkv_decode_kernel<W, B, FUSEQ, true, true>), grid,           \
+                         dim3(64 * W), 0, (hipStream_t)stream, a.block_table, (const void*)plan,  \
+                         FUSEQ ? (const void*)a.positions : (const void*)a.kc,                     \
+                         FUSEQ ? (const void*)a.slot_mapping : (const void*)a.vc, a.q,             \
+                         a.num_splits, a.max_blocks, a.bs_log2, a.n_kv, a);                        \
+    else if (plan)                                                                              \
       hipLaunchKernelGGL((smx::splitkv_decode_kernel<W, B, FUSEQ, true>), grid, dim3(64 * W),   \
                          0, (hipStream_t)stream, a.block_table, (const void*)plan,                \
                          FUSEQ ? (const void*)a.positions : (const void*)a.kc,                     \
