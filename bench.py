@@ -641,7 +641,7 @@ def main() -> int:
         print(json.dumps(counter_workload(dev)))
         return 0
     if args.phase == "batch":
-        print(json.dumps(batch_decode(dev)))
+        print(json.dumps(batch_decode(dev, breakdown=not args.skip_breakdown)))
         return 0
 
     if args.phase in ("all", "roofline"):
@@ -737,7 +737,7 @@ def main() -> int:
             f"(measured {tpot * 1e3:.4f} ms)")
     if args.phase == "all":
         log("batched decode (8 ragged sequences)")
-        out["batch_decode"] = batch_decode(dev)
+        out["batch_decode"] = batch_decode(dev, breakdown=not args.skip_breakdown)
         log(f"  {out['batch_decode']['tok_s']} tok/s aggregate")
     if not args.skip_cpu and args.phase in ("all", "cpu", "decode"):
         log("CPU baseline")
