@@ -838,6 +838,8 @@ int launch_merge(void* stream, const float* partial_o, const float* partial_lse,
   SMX_REQUIRE(n_kv >= 1 && n_q == 4 * n_kv && n_kv <= 65535, "need n_q == 4 * n_kv (GQA 4:1)"); \
   SMX_REQUIRE(block_size >= 32 && block_size <= 4096 && (block_size & (block_size - 1)) == 0,    \
               "block_size must be a power of two in [32, 4096]");                                \
+  SMX_REQUIRE((int64_t)max_blocks * block_size <= INT32_MAX,                                     \
+              "max_blocks * block_size (a sequence's capacity) must fit in int32");              \
   SMX_REQUIRE(scale > 0.f && isfinite(scale), "scale must be positive and finite");              \
   SMX_REQUIRE((uintptr_t)q % 16 == 0 && (uintptr_t)k_cache % 16 == 0 &&                          \
                   (uintptr_t)v_cache % 16 == 0 && (uintptr_t)block_table % 4 == 0 &&             \

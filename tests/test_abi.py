@@ -51,6 +51,7 @@ def test_bindings_cover_header():
     ("smx_splitkv_decode", (None, 16, 16, 16, 16, 16, 16, 16, 1, 4, 8, 8, 96, 32, 8, 128, 0.1)),
     ("smx_splitkv_decode", (None, 16, 16, 16, 16, 16, 16, 16, 1, 0, 8, 8, 128, 32, 8, 128, 0.1)),
     ("smx_splitkv_decode", (None, 16, 16, 16, 16, 16, 16, 16, 1, 4, 8, 8, 128, 32, 8, 128, -1.0)),
+    ("smx_splitkv_decode", (None, 16, 16, 16, 16, 16, 16, 16, 1, 4, 1 << 20, 8, 4096, 32, 8, 128, 0.1)),
     ("smx_lse_merge", (None, 16, 16, 16, 1, 0, 32, 128)),
     ("smx_lse_merge", (None, 16, 16, 16, 1, 4, 32, 64)),
     ("smx_splitkv_decode_merged", (None, 16, 16, 16, 16, 16, 16, 16, None, 1, 4, 8, 8, 128, 32, 8, 128, 0.1)),
