@@ -242,12 +242,17 @@ def test_plan_records_match_oracle(ops, dev, lengths, bs, items, splits):
     ([512, 3000, 77, 8192, 1, 0, 129], 128, 24, 16),
     ([512, 3000, 77, 8192, 1, 0, 129], 32, 56, 64),
     ([6144], 128, 49, 64), ([20000], 32, 1, 1), ([9000, 40], 128, 2, 2),
-    ([32768, 1, 20000], 128, 88, 16), (list(range(0, 64 * 11, 11)), 32, 100, 8)])
+    ([32768, 1, 20000], 128, 88, 16), (list(range(0, 64 * 11, 11)), 32, 100, 8),
+    # records (items + sequences) a multiple of 8: the records-fastest grid
+    ([512, 3000, 77, 8192, 1, 0, 129], 128, 25, 16), ([32768, 1, 20000], 128, 85, 16),
+    (list(range(0, 64 * 11, 11)), 32, 64, 8)])
 def test_planned_vs_fp64(ops, dev, lengths, bs, items, splits):
     """Merged outputs against float64 attention, every split's partial against
     the oracle's online softmax over the plan's bounds, and the slots no
     split writes cleared to (0, -inf).  ([20000] with 32-token pages and one
-    split: the waves' pages beyond the record's 55 come from the table.)"""
+    split: the waves' pages beyond the record's 55 come from the table.)
+    Plans whose record count is a multiple of 8 launch records fastest (all
+    kv heads of a record on one XCD), the others kv heads fastest."""
     rng = np.random.default_rng(sum(lengths) + items)
     q, kc, vc, table = _case(rng, [max(L, 1) for L in lengths], bs)
     scale = HD ** -0.5
