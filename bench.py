@@ -265,9 +265,48 @@ def build_model(dev, max_len: int, num_splits: int | None, seed: int = 0):
     return DecodeModel(DecoderConfig(), dev, seed=seed, max_len=max_len, num_splits=num_splits)
 
 
-def _timed_steps(model, n: int) -> float:
-    """Seconds for n graph replays, HIP events on the replay stream."""
+#: fences between two kernels of a step-runner replay: agent-scope acquire,
+#: no release (every kernel writes what a later one reads with agent-scope
+#: stores, so no boundary needs an L2 write-back)
+RUNNER_FENCES = "acquire"
+
+
+def record_runner(model):
+    """Record the model's decode step into a step runner; returns (executor,
+    reason): ("runner", None), or ("graph", why) when no runner could be made
+    (for instance no HSA queue), in which case the captured graph is timed."""
+    try:
+        model.record_runner()
+        return "runner", None
+    except Exception as exc:  # the graph executor still measures the same kernels
+        return "graph", f"{type(exc).__name__}: {exc}"
+
+
+EXECUTORS = {"runner": "step runner: AQL packets on the library's own HSA queue, agent-scope "
+                       "acquire and no release between kernels",
+             "graph": "HIP graph replay (agent-scope acquire and release between kernels)"}
+
+
+def _untimed_steps(model, n: int, executor: str = "graph") -> None:
+    if n <= 0:
+        return
+    if executor == "runner":
+        model.run_steps(n, RUNNER_FENCES)
+    else:
+        for _ in range(n):
+            model.step()
+
+
+def _timed_steps(model, n: int, executor: str = "graph") -> float:
+    """Seconds for n decode steps: n graph replays timed with HIP events on
+    the replay stream, or one step-runner replay of n steps timed by the
+    GPU's packet-processor timestamps (its first kernel's start to its last
+    kernel's end)."""
     import torch
+    if executor == "runner":
+        model.runner.replay(n, RUNNER_FENCES)  # synchronises the device first
+        model.runner.wait(120.0)
+        return model.runner.elapsed()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -279,14 +318,13 @@ def _timed_steps(model, n: int) -> float:
     return start.elapsed_time(end) * 1e-3
 
 
-def run_protocol(model, prompt, warmup: int, steps: int):
+def run_protocol(model, prompt, warmup: int, steps: int, executor: str = "graph"):
     """Feed the prompt, run `warmup` generated steps untimed, time `steps`;
     returns (seconds per step, tokens, positions timed)."""
     model.reset(prompt)
-    for _ in range(prompt.numel() - 1 + warmup):
-        model.step()
+    _untimed_steps(model, prompt.numel() - 1 + warmup, executor)
     p0 = prompt.numel() - 1 + warmup
-    dt = _timed_steps(model, steps)
+    dt = _timed_steps(model, steps, executor)
     total = prompt.numel() + warmup + steps
     return dt / steps, model.state.tokens[0, :total].clone().cpu(), list(range(p0, p0 + steps))
 
@@ -302,16 +340,15 @@ def spread_segments(steps: int, lo: int = PROMPT, hi: int = PROMPT + GENERATED -
     return [(lo + round(i * span / (n - 1)), lens[i]) for i in range(n)]
 
 
-def run_spread(model, warmup: int, segments):
+def run_spread(model, warmup: int, segments, executor: str = "graph"):
     """Time each segment's positions after `warmup` untimed steps before it,
     on the model's pre-filled KV cache; returns (seconds per step, tokens
     generated in the timed steps, positions timed)."""
     total_t, toks, positions = 0.0, [], []
     for p0, n in segments:
         model.set_context([p0 - warmup], ids=[1])
-        for _ in range(warmup):
-            model.step()
-        total_t += _timed_steps(model, n)
+        _untimed_steps(model, warmup, executor)
+        total_t += _timed_steps(model, n, executor)
         toks.append(model.state.tokens[0, p0 + 1:p0 + n + 1].clone().cpu())
         positions += list(range(p0, p0 + n))
     import torch
@@ -400,10 +437,18 @@ def batch_decode(dev, steps: int = 64, warmup: int = 4, batch: int = 8, seed: in
     model.fill_kv(seed)
     model.set_context(ctx.tolist())
     model.capture()
+    executor, runner_error = record_runner(model)
     model.set_context(ctx.tolist())
-    for _ in range(warmup):
-        model.step()
-    dt = _timed_steps(model, steps) / steps
+    _untimed_steps(model, warmup, executor)
+    dt = _timed_steps(model, steps, executor) / steps
+    toks = model.state.tokens.clone().cpu()
+    graph_dt = same = None
+    if executor == "runner":  # the same steps through the graph, for comparison
+        model.set_context(ctx.tolist())
+        _untimed_steps(model, warmup, "graph")
+        graph_dt = _timed_steps(model, steps, "graph") / steps
+        same = bool(torch.equal(toks, model.state.tokens.cpu()))
+        model.runner.close()
     c = model.cfg
     rb = lambda n, k: n * k // 32 * 18
     weights = c.n_layers * (rb(c.qkv_rows, c.hidden) + rb(c.hidden, c.n_q * c.head_dim)
@@ -416,7 +461,13 @@ def batch_decode(dev, steps: int = 64, warmup: int = 4, batch: int = 8, seed: in
     del model
     torch.cuda.empty_cache()
     extra = {"step_breakdown": bd} if bd else {}
+    if graph_dt is not None:
+        extra.update(graph_ms_per_step=round(graph_dt * 1e3, 4),
+                     tokens_equal_graph_vs_runner=same)
+    if runner_error:
+        extra["runner_error"] = runner_error
     return {**extra, "batch": batch, "contexts": ctx.tolist(), "steps": steps,
+            "executor": EXECUTORS[executor],
             "ms_per_step": round(dt * 1e3, 4),
             "tok_s": round(batch / dt, 2),
             # every sequence advances one token per step: its TPOT is the step time
@@ -668,6 +719,8 @@ def main() -> int:
     log(f"building the 4B model (block table {-(-max_len // 128)} pages)")
     model = build_model(dev, max_len, args.num_splits or None)
     model.capture()
+    executor, runner_error = record_runner(model)
+    log(f"executor: {EXECUTORS[executor]}" + (f" ({runner_error})" if runner_error else ""))
     c = model.cfg
     if protocol:
         prompt = torch.randint(0, c.vocab, (args.prompt_len,),
@@ -681,17 +734,26 @@ def main() -> int:
                f"{', '.join(f'{p}..{p + n - 1}' for p, n in segments)} (each after "
                f"{args.warmup} untimed tokens) over a seeded random KV cache, spread over the "
                f"protocol's {PROMPT + 1}..{PROMPT + GENERATED} contexts")
+    def one_run(ex):
+        if protocol:
+            return run_protocol(model, prompt, args.warmup, args.steps, ex)
+        return run_spread(model, args.warmup, segments, ex)
+
     tpots, token_runs = [], []
     for r in range(args.runs):
-        if protocol:
-            tpot, toks, positions = run_protocol(model, prompt, args.warmup, args.steps)
-        else:
-            tpot, toks, positions = run_spread(model, args.warmup, segments)
+        tpot, toks, positions = one_run(executor)
         tpots.append(tpot)
         token_runs.append(toks)
         log(f"run {r}: TPOT {tpot * 1e3:.4f} ms ({1 / tpot:.1f} tok/s)")
     tpot = statistics.median(tpots)
     deterministic = all(torch.equal(token_runs[0], t) for t in token_runs[1:])
+    graph_cmp = {}
+    if executor == "runner":  # the same steps once through the captured graph
+        g_tpot, g_toks, _ = one_run("graph")
+        graph_cmp = {"graph_ms_per_step": round(g_tpot * 1e3, 4),
+                     "tokens_equal_graph_vs_runner": bool(torch.equal(g_toks, token_runs[0]))}
+        log(f"graph: TPOT {g_tpot * 1e3:.4f} ms")
+        model.runner.close()
     gen = token_runs[0][args.prompt_len:] if protocol else token_runs[0]
     valid = bool(((gen >= 0) & (gen < c.vocab)).all())
     mean_bytes = statistics.fmean(step_bytes(c, p + 1) for p in positions)
@@ -717,6 +779,9 @@ def main() -> int:
                    "contexts": [min(positions) + 1, max(positions) + 1],
                    "mean_context": round(statistics.fmean(positions) + 1, 1),
                    "parallelism": "single GPU", "num_splits": model.num_splits},
+        "executor": EXECUTORS[executor],
+        **graph_cmp,
+        **({"runner_error": runner_error} if runner_error else {}),
         "tpot_ms_runs": [round(t * 1e3, 4) for t in tpots],
         "tokens_deterministic_across_runs": deterministic,
         "tokens_in_vocab": valid,
@@ -732,9 +797,10 @@ def main() -> int:
         log("step breakdown (each kernel class alone, at the timed steps' mean context)")
         out["step_breakdown"] = step_breakdown(model, int(round(statistics.fmean(positions))) + 1)
         sb = out["step_breakdown"]
-        sb["measured_ms"] = round(tpot * 1e3, 4)
+        # the breakdown replays graphs: set it against the graph executor's step
+        sb["measured_ms"] = graph_cmp.get("graph_ms_per_step", round(tpot * 1e3, 4))
         log(f"  per layer {sb['us_per_layer']} us; per step {sb['per_step_sum_ms']} ms "
-            f"(measured {tpot * 1e3:.4f} ms)")
+            f"(graph step measured {sb['measured_ms']} ms)")
     if args.phase == "all":
         log("batched decode (8 ragged sequences)")
         out["batch_decode"] = batch_decode(dev, breakdown=not args.skip_breakdown)

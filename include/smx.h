@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define SMX_ABI_VERSION 6
+#define SMX_ABI_VERSION 7
 
 /* Return codes besides 0 and hipError_t values. */
 #define SMX_EINVAL 10001      /* an argument failed validation */
@@ -457,6 +457,50 @@ int smx_decode_advance(void* stream, int64_t* next_ids,
 int64_t smx_read_probe_sink_size(int64_t bytes, int32_t loads_per_lane);
 int smx_read_probe(void* stream, const void* src, int64_t bytes, uint32_t* sink,
                    int64_t sink_size, int32_t loads_per_lane);
+
+/*
+ * Step runner: records the kernel launches that the C-ABI calls made on the
+ * calling thread between smx_runner_begin and smx_runner_end would enqueue
+ * (nothing is launched meanwhile; the calls still validate their arguments
+ * and return their codes), then replays them as AQL kernel-dispatch packets
+ * on an HSA queue of its own.  It serves the loop the reference runs as one
+ * graph replay per decode step (src/spark_vllm_ascend/plugin/spark2_5.py:
+ * 369-376): a step that is device-driven (positions, slots and the next
+ * token advance on the device) replays `repeats` times in one call.
+ *
+ * code_objects: paths of this library's device code objects (one per source
+ * file, built beside the library).  The runner binds to the HSA agent of the
+ * current HIP device.  Recording keeps raw pointers: every buffer a recorded
+ * call names must outlive the recording's replays.  A replay starts with a
+ * system-scope acquire (it sees all work the host and the HIP streams have
+ * completed; the caller synchronises them first) and ends with a
+ * system-scope release (smx_runner_wait then makes every result visible to
+ * the host).  Between two of its kernels:
+ *   SMX_RUNNER_FENCES_AGENT         agent-scope acquire and release, the
+ *                                   fences of a HIP stream or graph;
+ *   SMX_RUNNER_FENCES_ACQUIRE_ONLY  agent-scope acquire, no release: valid
+ *                                   only because every kernel of this
+ *                                   library writes what a later kernel
+ *                                   reads with agent-scope stores and waits
+ *                                   for them before its waves end.
+ * One runner per thread at a time; calls on one runner must not overlap.
+ */
+#define SMX_RUNNER_FENCES_AGENT 0
+#define SMX_RUNNER_FENCES_ACQUIRE_ONLY 1
+typedef struct smx_runner smx_runner;
+int smx_runner_create(const char* const* code_objects, int32_t count, smx_runner** out);
+int smx_runner_begin(smx_runner* runner);
+int smx_runner_end(smx_runner* runner);
+int smx_runner_num_packets(const smx_runner* runner, int64_t* out);
+/* Enqueue the recorded packets `repeats` times and return; 0 or SMX_EINVAL. */
+int smx_runner_replay(smx_runner* runner, int32_t repeats, int32_t fences);
+/* Wait until every replay has completed, or fail after timeout_s seconds. */
+int smx_runner_wait(smx_runner* runner, double timeout_s);
+/* GPU time of the last replay, from its first kernel's start to its last
+ * kernel's end (packet-processor timestamps), once it has completed. */
+int smx_runner_elapsed(smx_runner* runner, double* seconds);
+/* Waits (at most 60 s) for running replays, then frees the runner. */
+void smx_runner_destroy(smx_runner* runner);
 
 #ifdef __cplusplus
 }

@@ -209,6 +209,7 @@ class DecodeModel:
         self.argmax_keys = (torch.empty((B, nk), dtype=torch.int64, device=dev) if nk > 0
                             else None)
         self.graph: torch.cuda.CUDAGraph | None = None
+        self.runner = None  # native.runner.StepRunner after record_runner()
 
     @classmethod
     def from_gguf(cls, path, device, max_len: int = 8192, num_splits: int | None = None,
@@ -302,12 +303,17 @@ class DecodeModel:
                                         out=self.logits)
             keys = self.argmax_keys
         elif self.batch > 1 and self.argmax_keys is not None:
-            ops.add_rmsnorm(x_in, r_in, self.final_norm, c.eps, out=self.h)
+            # the final norm's residual output is unused: res_a (free after
+            # the last layer's post norm) takes it, so the step allocates
+            # nothing (a recorded step must not, see record_runner)
+            ops.add_rmsnorm(x_in, r_in, self.final_norm, c.eps, out=self.h,
+                            residual_out=self.res_a)
             ops.q4_0_gemm_argmax(self.h, self.head.q4_0_head, c.vocab, c.hidden,
                                  self.argmax_keys, out=self.logits)
             keys = self.argmax_keys
         else:
-            ops.add_rmsnorm(x_in, r_in, self.final_norm, c.eps, out=self.h)
+            ops.add_rmsnorm(x_in, r_in, self.final_norm, c.eps, out=self.h,
+                            residual_out=self.res_a)
             ops.q4_0_gemv(self.h, self.head.q4_0_head, c.vocab, c.hidden, out=self.logits)
             ops.argmax(self.logits, out=st.next_ids)
         ops.decode_advance(st.next_ids, st.ids, st.positions, st.seq_lens, st.slot_mapping,
@@ -328,6 +334,22 @@ class DecodeModel:
         with torch.cuda.graph(g):
             self.enqueue_step()
         self.graph = g
+
+    def record_runner(self, runner=None):
+        """Record one decode step into a step runner (native/runner.py): the
+        counterpart of capture() that replays the step's kernels as AQL
+        dispatch packets on a queue of the library's own.  Recording launches
+        nothing and leaves the decode state as it is."""
+        from ..native.runner import StepRunner
+        self.runner = runner if runner is not None else StepRunner()
+        self.runner.record(self.enqueue_step)
+        return self.runner
+
+    def run_steps(self, n: int, fences: str = "agent", timeout_s: float = 60.0) -> None:
+        """n decode steps through the recorded runner, waiting for them."""
+        if self.runner is None:
+            raise RuntimeError("record_runner() first")
+        self.runner.run(n, fences, timeout_s)
 
     def step(self) -> None:
         if self.graph is not None:

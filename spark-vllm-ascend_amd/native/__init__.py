@@ -23,7 +23,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libsmx.so"
 #: spark-vllm-ascend_amd/native/validate.py after a passing GPU test run) to
 #: vouch for the library about to be loaded
 VALIDATION_ENV = "SMX_VALIDATION_RECORD"
-ABI_VERSION = 6
+ABI_VERSION = 7
 SMX_EINVAL = 10001
 SMX_EUNSUPPORTED = 10002
 
@@ -31,6 +31,7 @@ _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
 _I32 = ctypes.c_int32
 _F32 = ctypes.c_float
+_F64 = ctypes.c_double
 
 # name -> argument types (all return int)
 SIGNATURES = {
@@ -74,12 +75,25 @@ SIGNATURES = {
     "smx_q4_0_argmax_keys_size": [_I64, _I64],
     "smx_read_probe_sink_size": [_I64, _I32],
     "smx_read_probe": [_P, _P, _I64, _P, _I64, _I32],
+    "smx_runner_create": [ctypes.POINTER(ctypes.c_char_p), _I32, ctypes.POINTER(_P)],
+    "smx_runner_begin": [_P],
+    "smx_runner_end": [_P],
+    "smx_runner_num_packets": [_P, ctypes.POINTER(_I64)],
+    "smx_runner_replay": [_P, _I32, _I32],
+    "smx_runner_wait": [_P, _F64],
+    "smx_runner_elapsed": [_P, ctypes.POINTER(_F64)],
+    "smx_runner_destroy": [_P],
 }
+
+#: fence modes of smx_runner_replay (include/smx.h)
+RUNNER_FENCES_AGENT = 0
+RUNNER_FENCES_ACQUIRE_ONLY = 1
 
 # return types other than int
 RESTYPES = {"smx_q4_0_argmax_keys_size": ctypes.c_int64,
             "smx_q4_0_gemm_keys_per_row": ctypes.c_int64,
-            "smx_read_probe_sink_size": ctypes.c_int64}
+            "smx_read_probe_sink_size": ctypes.c_int64,
+            "smx_runner_destroy": None}
 
 _lib = None
 

@@ -2,7 +2,9 @@
 
 Every HIP source is compiled for gfx950 only, with packed-FP32 code
 generation disabled, and linked into ``native/libsmx.so`` next to this file.
-Run as ``python build.py`` or call :func:`build`.
+Each HIP source's device code is also written as a code object
+(``native/libsmx.<source>.co``), which the step runner loads into its own
+HSA executables.  Run as ``python build.py`` or call :func:`build`.
 """
 from __future__ import annotations
 
@@ -19,6 +21,7 @@ LIB = HERE / "libsmx.so"
 OBJ_DIR = HERE / "_build"
 
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
+ROCM_LIB = Path(os.environ.get("ROCM_PATH", "/opt/rocm")) / "lib"
 COMMON = [
     "--offload-arch=gfx950",
     "-O3",
@@ -32,7 +35,13 @@ COMMON = [
     "-mllvm", "-amdgpu-kernarg-preload-count=16",
 ]
 SOURCES = ["q4_0_gemv.hip", "q4_0_gemm.hip", "splitkv_attention.hip", "small_ops.hip",
-           "read_probe.hip", "abi.cpp"]
+           "read_probe.hip", "abi.cpp", "step_runner.cpp"]
+DEVICE_SOURCES = [s for s in SOURCES if s.endswith(".hip")]
+
+
+def code_object_paths() -> list[Path]:
+    """The device code objects the step runner loads, one per HIP source."""
+    return [HERE / f"libsmx.{Path(s).stem}.co" for s in DEVICE_SOURCES]
 
 
 def _compile(src: str) -> Path:
@@ -45,13 +54,31 @@ def _compile(src: str) -> Path:
     return out
 
 
+def _code_object(src: str) -> Path:
+    out = HERE / f"libsmx.{Path(src).stem}.co"
+    tmp = out.with_suffix(".co.tmp")
+    cmd = [HIPCC, *COMMON, "-x", "hip", "--cuda-device-only", "--no-gpu-bundle-output",
+           str(CSRC / src), "-o", str(tmp)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc (device code object) failed for {src}:\n{res.stderr}")
+    os.replace(tmp, out)
+    return out
+
+
 def build(verbose: bool = False) -> Path:
-    """Compile all sources and link libsmx.so; returns the library path."""
+    """Compile all sources, link libsmx.so and write the device code objects;
+    returns the library path."""
     OBJ_DIR.mkdir(exist_ok=True)
     with concurrent.futures.ThreadPoolExecutor(max_workers=len(SOURCES)) as pool:
-        objs = list(pool.map(_compile, SOURCES))
+        objs_f = [pool.submit(_compile, s) for s in SOURCES]
+        cos_f = [pool.submit(_code_object, s) for s in DEVICE_SOURCES]
+        objs = [f.result() for f in objs_f]
+        for f in cos_f:
+            f.result()
     tmp = LIB.with_suffix(".so.tmp")
-    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp),
+           f"-L{ROCM_LIB}", f"-Wl,-rpath,{ROCM_LIB}", "-lhsa-runtime64"]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")

@@ -22,6 +22,7 @@
 //    block's nibbles start 2 bytes into a dword; its group-0 word is spliced
 //    from the pair's dwords 0 and 4 (elements 14, 15, 0, 1).
 #include "smx_common.h"
+#include "smx_launch.h"
 
 namespace smx {
 namespace {
@@ -144,14 +145,15 @@ __global__ __launch_bounds__(512) void q4_0_gemm_kernel(GemmArgs a) {
         if (nn < 8 && f < a.n_out) {
           const float gb = round_bf16(total(nn));
           const float ub = round_bf16(total(nn + 8));
-          a.y[(int64_t)m * a.ldy + f] = f32_to_bf16(gb / (1.0f + expf(-gb)) * ub);
+          st_agent(a.y + (int64_t)m * a.ldy + f, f32_to_bf16(gb / (1.0f + expf(-gb)) * ub));
         }
       } else {
         const int o = blockIdx.x * 16 + nn;
-        if (o < a.n_out) a.y[(int64_t)m * a.ldy + o] = f32_to_bf16(total(nn));
+        if (o < a.n_out) st_agent(a.y + (int64_t)m * a.ldy + o, f32_to_bf16(total(nn)));
       }
     }
   }
+  stores_done();
 }
 
 
@@ -199,6 +201,7 @@ template <bool SWIGLU, int WS, bool KEYS = false>
 __global__ __launch_bounds__(1024) void q4_0_gemm_tile_kernel(
     const uint8_t* w_, const uint16_t* x_, int npairs, int n_out, int64_t up_offset_rows, int ks,
     int m, int64_t ldx, uint16_t* y, int64_t ldy, uint64_t* keys) {
+  static_assert(!(SWIGLU && KEYS), "argmax keys are for plain outputs");
   __shared__ f32x4 red[16][64];
   extern __shared__ u32x4 xsl[];  // WS > 0: [ks][8 rows x 32 chunks]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -316,11 +319,11 @@ __global__ __launch_bounds__(1024) void q4_0_gemm_tile_kernel(
         if (nn < 8 && f < n_out) {
           const float gb = round_bf16(total(nn));
           const float ub = round_bf16(total(nn + 8));
-          y[(int64_t)mr * ldy + f] = f32_to_bf16(gb / (1.0f + expf(-gb)) * ub);
+          st_agent(y + (int64_t)mr * ldy + f, f32_to_bf16(gb / (1.0f + expf(-gb)) * ub));
         }
       } else {
         const int o = blockIdx.x * 16 + nn;
-        if (o < n_out) y[(int64_t)mr * ldy + o] = f32_to_bf16(total(nn));
+        if (o < n_out) st_agent(y + (int64_t)mr * ldy + o, f32_to_bf16(total(nn)));
       }
     }
     if constexpr (KEYS && !SWIGLU) {
@@ -337,9 +340,11 @@ __global__ __launch_bounds__(1024) void q4_0_gemm_tile_kernel(
             (uint32_t)__shfl_xor((int)(uint32_t)key, s, 64);
         key = other > key ? other : key;
       }
-      if (nn == 0 && mr < m) keys[(int64_t)mr * gridDim.x + blockIdx.x] = key;
+      // one key per row and 16-column group (the grid is ceil(n_out / 16) workgroups)
+      if (nn == 0 && mr < m) st_agent(keys + (int64_t)mr * ((n_out + 15) / 16) + blockIdx.x, key);
     }
   }
+  stores_done();
 }
 
 template <bool SWIGLU, bool KEYS = false>
@@ -365,7 +370,7 @@ hipError_t launch_gemm_tile(hipStream_t s, const void* x, const void* w, void* y
   if (const char* e = tuning_env("SMX_GEMM_WS")) ws = atoi(e) ? ws : 0;  // tuning sweeps
   const size_t lds = ws ? (size_t)ks * 256 * 16 : 0;
 #define SMX_GEMM_LAUNCH(W)                                                                      \
-  hipLaunchKernelGGL((q4_0_gemm_tile_kernel<SWIGLU, W, KEYS>), dim3(grid), dim3(64 * ks), lds,  \
+  SMX_LAUNCH((q4_0_gemm_tile_kernel<SWIGLU, W, KEYS>), dim3(grid), dim3(64 * ks), lds,  \
                      s, (const uint8_t*)w, (const uint16_t*)x, npairs, (int)n_out,                \
                      up_offset_rows, ks, (int)m, k, (uint16_t*)y, n_out, keys)
   if (ws == 1) SMX_GEMM_LAUNCH(1);
@@ -396,7 +401,7 @@ extern "C" int smx_q4_0_gemm(void* stream, const void* x, const void* w, void* y
     return (int)smx::launch_gemm_tile<false>((hipStream_t)stream, x, w, y, m, n, k, 0);
   smx::GemmArgs a{(const uint16_t*)x, (const uint8_t*)w, (uint16_t*)y, (int)m, (int)n,
                   (int)(k / 64), k, n, 0};
-  hipLaunchKernelGGL(smx::q4_0_gemm_kernel<false>, dim3((unsigned)((n + 15) / 16)), dim3(512), 0,
+  SMX_LAUNCH(smx::q4_0_gemm_kernel<false>, dim3((unsigned)((n + 15) / 16)), dim3(512), 0,
                      (hipStream_t)stream, a);
   return (int)hipGetLastError();
 }
@@ -408,7 +413,7 @@ extern "C" int smx_q4_0_gemm_swiglu(void* stream, const void* x, const void* w, 
     return (int)smx::launch_gemm_tile<true>((hipStream_t)stream, x, w, y, m, d, k, d);
   smx::GemmArgs a{(const uint16_t*)x, (const uint8_t*)w, (uint16_t*)y, (int)m, (int)d,
                   (int)(k / 64), k, d, d};
-  hipLaunchKernelGGL(smx::q4_0_gemm_kernel<true>, dim3((unsigned)((d + 7) / 8)), dim3(512), 0,
+  SMX_LAUNCH(smx::q4_0_gemm_kernel<true>, dim3((unsigned)((d + 7) / 8)), dim3(512), 0,
                      (hipStream_t)stream, a);
   return (int)hipGetLastError();
 }

@@ -27,6 +27,7 @@
 #include <math.h>
 
 #include "smx_common.h"
+#include "smx_launch.h"
 
 namespace smx {
 namespace {
@@ -261,7 +262,7 @@ __global__ __launch_bounds__(NPMAX <= 2 ? 1024 : 512) void q4_0_gemv_kernel(
       xv[t] = u32x4{yo[0], yo[1], yo[2], yo[3]};
       const int c = (wave + ks * t) * 64 + lane;
       if (write_res && c < nchunks)
-        reinterpret_cast<u32x4*>(a.residual_out)[c] = u32x4{ro[0], ro[1], ro[2], ro[3]};
+        st_agent(reinterpret_cast<u32x4*>(a.residual_out) + c, u32x4{ro[0], ro[1], ro[2], ro[3]});
     }
   }
 
@@ -322,13 +323,13 @@ __global__ __launch_bounds__(NPMAX <= 2 ? 1024 : 512) void q4_0_gemv_kernel(
           for (int i = 0; i < ks; ++i) up += part[i * (8 * RG) + g * 8 + r + 4];
           const float gb = round_bf16(tot);
           const float ub = round_bf16(up);
-          a.y[o] = f32_to_bf16(gb / (1.0f + expf(-gb)) * ub);
+          st_agent(a.y + o, f32_to_bf16(gb / (1.0f + expf(-gb)) * ub));
         }
       } else {
         const int o = (blockIdx.x * RG + g) * 8 + r;
         if (o < n_out) {
           const uint16_t yb = f32_to_bf16(tot);
-          a.y[o] = yb;
+          st_agent(a.y + o, yb);
           key = ((uint64_t)bf16_order_key(yb) << 32) | (uint64_t)(0xffffffffu - (uint32_t)o);
         }
       }
@@ -339,9 +340,10 @@ __global__ __launch_bounds__(NPMAX <= 2 ? 1024 : 512) void q4_0_gemv_kernel(
                                (uint32_t)__shfl_xor((int)(uint32_t)key, m, 64);
         key = other > key ? other : key;
       }
-      if (lane == 0) a.argmax_keys[blockIdx.x] = key;
+      if (lane == 0) st_agent(a.argmax_keys + blockIdx.x, key);
     }
   }
+  stores_done();
 }
 
 // Any k % 32 == 0 and any 2-byte alignment: one wave per output row, lanes
@@ -384,17 +386,18 @@ __global__ __launch_bounds__(64) void q4_0_gemv_generic_kernel(
     if constexpr (SWIGLU) {
       const float gb = round_bf16(acc[0]);
       const float ub = round_bf16(acc[1]);
-      y[o] = f32_to_bf16(gb / (1.0f + expf(-gb)) * ub);
+      st_agent(y + o, f32_to_bf16(gb / (1.0f + expf(-gb)) * ub));
     } else {
-      y[o] = f32_to_bf16(acc[0]);
+      st_agent(y + o, f32_to_bf16(acc[0]));
     }
   }
+  stores_done();
 }
 
 // One thread per block: 32 bf16 = RNE(float(d) * (nibble - 8)), exact product.
 __global__ __launch_bounds__(256) void q4_0_dequant_kernel(
     const uint8_t* __restrict__ w, uint16_t* __restrict__ out, int64_t total_blocks) {
-  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t b = (int64_t)blockIdx.x * 256 + threadIdx.x;  // 256 threads per workgroup
   if (b >= total_blocks) return;
   const uint16_t* blk = reinterpret_cast<const uint16_t*>(w + 18 * b);
   const float d = f16_bits_to_f32(blk[0]);
@@ -406,9 +409,10 @@ __global__ __launch_bounds__(256) void q4_0_dequant_kernel(
     const float l1 = d * (float)((int)((two >> 8) & 15u) - 8);
     const float h0 = d * (float)((int)((two >> 4) & 15u) - 8);
     const float h1 = d * (float)((int)((two >> 12) & 15u) - 8);
-    o[i] = pack_bf16x2(l0, l1);
-    o[8 + i] = pack_bf16x2(h0, h1);
+    st_agent(o + i, pack_bf16x2(l0, l1));
+    st_agent(o + 8 + i, pack_bf16x2(h0, h1));
   }
+  stores_done();
 }
 
 }  // namespace
@@ -423,7 +427,7 @@ static hipError_t launch_fast(hipStream_t s, const GemvArgs& a, int ks) {
   const int grid = (a.n_out + OUT_PER_WG - 1) / OUT_PER_WG;
   const size_t lds = (size_t)ks * NPMAX * 8 * 36 * 4 + (size_t)ks * 8 * RG * 4 + (size_t)ks * 4;
   const GemvTail tail{a.residual_out, a.y, a.argmax_keys, a.eps};
-  hipLaunchKernelGGL((q4_0_gemv_kernel<NPMAX, RG, PRO, EPI>), dim3(grid), dim3(64 * ks), lds, s,
+  SMX_LAUNCH((q4_0_gemv_kernel<NPMAX, RG, PRO, EPI>), dim3(grid), dim3(64 * ks), lds, s,
                      a.w, a.x, a.residual, a.gamma, a.npairs, a.n_out, a.up_offset_rows, ks,
                      tail);
   return hipGetLastError();
@@ -543,10 +547,10 @@ static hipError_t gemv_dispatch(hipStream_t s, GemvArgs a, int64_t k, int epi, b
   if (!fast_path(k, a.x, a.w, &sh, a.n_out, epi == EPI_SWIGLU ? 4 : 8, kind)) {
     if (pro || epi == EPI_ARGMAX) return hipErrorInvalidValue;  // callers check first
     if (epi == EPI_SWIGLU)
-      hipLaunchKernelGGL(q4_0_gemv_generic_kernel<true>, dim3((unsigned)a.n_out), dim3(64), 0, s,
+      SMX_LAUNCH(q4_0_gemv_generic_kernel<true>, dim3((unsigned)a.n_out), dim3(64), 0, s,
                          a.x, a.w, a.y, a.n_out, (int)nblocks, a.up_offset_rows);
     else
-      hipLaunchKernelGGL(q4_0_gemv_generic_kernel<false>, dim3((unsigned)a.n_out), dim3(64), 0,
+      SMX_LAUNCH(q4_0_gemv_generic_kernel<false>, dim3((unsigned)a.n_out), dim3(64), 0,
                          s, a.x, a.w, a.y, a.n_out, (int)nblocks, a.up_offset_rows);
     return hipGetLastError();
   }
@@ -573,7 +577,7 @@ extern "C" int smx_q4_0_dequant_bf16(void* stream, const void* w, void* out, int
   const int64_t total = n * (k / 32);
   const int64_t grid = (total + 255) / 256;
   SMX_REQUIRE(grid < (1ll << 31), "tensor too large");
-  hipLaunchKernelGGL(smx::q4_0_dequant_kernel, dim3((unsigned)grid), dim3(256), 0,
+  SMX_LAUNCH(smx::q4_0_dequant_kernel, dim3((unsigned)grid), dim3(256), 0,
                      (hipStream_t)stream, (const uint8_t*)w, (uint16_t*)out, total);
   return (int)hipGetLastError();
 }

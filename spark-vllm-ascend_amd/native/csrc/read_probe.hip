@@ -6,6 +6,7 @@
 // has the same launch and first-load latency and no arithmetic.  No
 // counterpart in the reference (a measurement instrument).
 #include "smx_common.h"
+#include "smx_launch.h"
 
 namespace smx {
 namespace {
@@ -25,7 +26,8 @@ __global__ __launch_bounds__(256) void read_probe_kernel(const u32x4* __restrict
   for (int i = 0; i < LOADS; ++i) x ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) x ^= (uint32_t)__shfl_xor((int)x, o, 64);
-  if ((threadIdx.x & 63) == 0) sink[blockIdx.x * 4 + (threadIdx.x >> 6)] = x;  // lane 0 of each wave
+  if ((threadIdx.x & 63) == 0) st_agent(sink + blockIdx.x * 4 + (threadIdx.x >> 6), x);  // lane 0 of each wave
+  stores_done();
 }
 
 }  // namespace
@@ -57,11 +59,11 @@ extern "C" int smx_read_probe(void* stream, const void* src, int64_t bytes, uint
   const hipStream_t s = (hipStream_t)stream;
   const auto* p = reinterpret_cast<const smx::u32x4*>(src);
   switch (loads_per_lane) {
-    case 1: hipLaunchKernelGGL(smx::read_probe_kernel<1>, dim3((unsigned)grid), dim3(256), 0, s, p, n16, sink); break;
-    case 2: hipLaunchKernelGGL(smx::read_probe_kernel<2>, dim3((unsigned)grid), dim3(256), 0, s, p, n16, sink); break;
-    case 4: hipLaunchKernelGGL(smx::read_probe_kernel<4>, dim3((unsigned)grid), dim3(256), 0, s, p, n16, sink); break;
-    case 8: hipLaunchKernelGGL(smx::read_probe_kernel<8>, dim3((unsigned)grid), dim3(256), 0, s, p, n16, sink); break;
-    default: hipLaunchKernelGGL(smx::read_probe_kernel<16>, dim3((unsigned)grid), dim3(256), 0, s, p, n16, sink); break;
+    case 1: SMX_LAUNCH(smx::read_probe_kernel<1>, dim3((unsigned)grid), dim3(256), 0, s, p, n16, sink); break;
+    case 2: SMX_LAUNCH(smx::read_probe_kernel<2>, dim3((unsigned)grid), dim3(256), 0, s, p, n16, sink); break;
+    case 4: SMX_LAUNCH(smx::read_probe_kernel<4>, dim3((unsigned)grid), dim3(256), 0, s, p, n16, sink); break;
+    case 8: SMX_LAUNCH(smx::read_probe_kernel<8>, dim3((unsigned)grid), dim3(256), 0, s, p, n16, sink); break;
+    default: SMX_LAUNCH(smx::read_probe_kernel<16>, dim3((unsigned)grid), dim3(256), 0, s, p, n16, sink); break;
   }
   return (int)hipGetLastError();
 }

@@ -6,15 +6,15 @@
 #include <math.h>
 
 #include "smx_common.h"
+#include "smx_launch.h"
 
 namespace smx {
 namespace {
 
-// Block-wide sum for up to 1024 threads (wave sums, then LDS).
-__device__ __forceinline__ float block_sum(float v, float* red) {
+// Block-wide sum over the nw waves of a workgroup (wave sums, then LDS).
+__device__ __forceinline__ float block_sum(float v, float* red, int nw) {
   v = wave_sum(v);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int nw = (blockDim.x + 63) >> 6;
   if (lane == 0) red[wave] = v;
   __syncthreads();
   float t = 0.f;
@@ -31,10 +31,12 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 // indices, so the row costs one round trip before the reduction (loads under
 // a branch, or gamma loaded after the reduction, each cost another).  Each
 // thread writes only the indices it read, so residual_out may alias residual.
+// nt = the workgroup size (a multiple of 64), passed rather than read from
+// blockDim so the kernel takes no implicit arguments.
 template <int CH, bool RES>
 __global__ __launch_bounds__(1024) void add_rmsnorm_kernel(
     const uint16_t* __restrict__ x, const uint16_t* residual, const uint16_t* __restrict__ gamma,
-    uint16_t* __restrict__ y, uint16_t* residual_out, int hidden, float eps) {
+    uint16_t* __restrict__ y, uint16_t* residual_out, int hidden, float eps, int nt) {
   __shared__ float red[16];
   const int64_t row = blockIdx.x;
   const u32x4* xr = reinterpret_cast<const u32x4*>(x + row * hidden);
@@ -44,7 +46,7 @@ __global__ __launch_bounds__(1024) void add_rmsnorm_kernel(
   u32x4 xa[CH], ra[CH], ga[CH];
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
-    const int ch = min((int)threadIdx.x + c * (int)blockDim.x, nch - 1);
+    const int ch = min((int)threadIdx.x + c * nt, nch - 1);
     xa[c] = xr[ch];
     if constexpr (RES) ra[c] = rr[ch];
     ga[c] = gr[ch];
@@ -53,7 +55,7 @@ __global__ __launch_bounds__(1024) void add_rmsnorm_kernel(
   float ss = 0.f;
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
-    const bool ok = (int)threadIdx.x + c * (int)blockDim.x < nch;
+    const bool ok = (int)threadIdx.x + c * nt < nch;
     const uint32_t aw[4] = {xa[c].x, xa[c].y, xa[c].z, xa[c].w};
     const uint32_t bw[4] = {ra[c].x, ra[c].y, ra[c].z, ra[c].w};
 #pragma unroll
@@ -63,11 +65,11 @@ __global__ __launch_bounds__(1024) void add_rmsnorm_kernel(
       if (ok) ss += sv[c][2 * i] * sv[c][2 * i] + sv[c][2 * i + 1] * sv[c][2 * i + 1];
     }
   }
-  ss = block_sum(ss, red);
+  ss = block_sum(ss, red, nt >> 6);
   const float inv = 1.0f / sqrtf(ss / (float)hidden + eps);
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
-    const int ch = (int)threadIdx.x + c * (int)blockDim.x;
+    const int ch = (int)threadIdx.x + c * nt;
     if (ch < nch) {
       const uint32_t gw[4] = {ga[c].x, ga[c].y, ga[c].z, ga[c].w};
       uint32_t yo[4], ro[4];
@@ -77,11 +79,13 @@ __global__ __launch_bounds__(1024) void add_rmsnorm_kernel(
         ro[i] = pack_bf16x2(s0, s1);
         yo[i] = pack_bf16x2(s0 * inv * bf16_lo(gw[i]), s1 * inv * bf16_hi(gw[i]));
       }
-      reinterpret_cast<u32x4*>(y + row * hidden)[ch] = u32x4{yo[0], yo[1], yo[2], yo[3]};
+      st_agent(reinterpret_cast<u32x4*>(y + row * hidden) + ch, u32x4{yo[0], yo[1], yo[2], yo[3]});
       if (residual_out)
-        reinterpret_cast<u32x4*>(residual_out + row * hidden)[ch] = u32x4{ro[0], ro[1], ro[2], ro[3]};
+        st_agent(reinterpret_cast<u32x4*>(residual_out + row * hidden) + ch,
+                 u32x4{ro[0], ro[1], ro[2], ro[3]});
     }
   }
+  stores_done();
 }
 
 // One wave per (head, token).  head_dim = 128: lane i owns dims i and i + 64,
@@ -108,9 +112,10 @@ __global__ __launch_bounds__(64) void qknorm_rope_kv_kernel(
   if (h >= n_q + n_kv) {  // v head
     if (write_kv) {
       uint16_t* dst = v_cache + (slot * n_kv + (h - n_q - n_kv)) * HD;
-      dst[lane] = src[lane];
-      dst[lane + HALF] = src[lane + HALF];
+      st_agent(dst + lane, src[lane]);
+      st_agent(dst + lane + HALF, src[lane + HALF]);
     }
+    stores_done();
     return;
   }
   const uint16_t* gam = h < n_q ? q_gamma : k_gamma;
@@ -127,37 +132,40 @@ __global__ __launch_bounds__(64) void qknorm_rope_kv_kernel(
   const uint16_t v = f32_to_bf16(b * c + a * s);
   if (h < n_q) {
     uint16_t* dst = q_out + ((int64_t)t * n_q + h) * HD;
-    dst[lane] = u;
-    dst[lane + HALF] = v;
+    st_agent(dst + lane, u);
+    st_agent(dst + lane + HALF, v);
   } else if (write_kv) {
     uint16_t* dst = k_cache + (slot * n_kv + (h - n_q)) * HD;
-    dst[lane] = u;
-    dst[lane + HALF] = v;
+    st_agent(dst + lane, u);
+    st_agent(dst + lane + HALF, v);
   }
+  stores_done();
 }
 
 // out = bf16(silu(g) * u) with silu(g) = g / (1 + exp(-g)), all in fp32.
 __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restrict__ gu,
                                                        uint16_t* __restrict__ out, int64_t rows,
                                                        int64_t d) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // 256 threads per workgroup
   if (i >= rows * d) return;
   const int64_t r = i / d, c = i % d;
   const float g = bf16_bits_to_f32(gu[r * 2 * d + c]);
   const float u = bf16_bits_to_f32(gu[r * 2 * d + d + c]);
-  out[i] = f32_to_bf16(g / (1.0f + expf(-g)) * u);
+  st_agent(out + i, f32_to_bf16(g / (1.0f + expf(-g)) * u));
+  stores_done();
 }
 
 __global__ __launch_bounds__(256) void embedding_kernel(const uint16_t* __restrict__ table,
                                                         const int64_t* __restrict__ ids,
                                                         uint16_t* __restrict__ out, int64_t vocab,
-                                                        int64_t hidden) {
+                                                        int64_t hidden, int gx) {
+  // gx workgroups of 256 threads along x (passed: no implicit arguments)
   const int64_t t = blockIdx.y;
   const int64_t id = ids[t];
   const bool ok = id >= 0 && id < vocab;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < hidden;
-       i += (int64_t)gridDim.x * blockDim.x)
-    out[t * hidden + i] = ok ? table[id * hidden + i] : (uint16_t)0;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < hidden; i += (int64_t)gx * 256)
+    st_agent(out + t * hidden + i, ok ? table[id * hidden + i] : (uint16_t)0);
+  stores_done();
 }
 
 // (value, index) ordering for argmax: larger value wins, NaN is largest,
@@ -172,6 +180,7 @@ __device__ __forceinline__ bool better(float v, int64_t i, float bv, int64_t bi)
 // One 1024-thread workgroup per row.
 __global__ __launch_bounds__(1024) void argmax_kernel(const uint16_t* __restrict__ logits,
                                                       int64_t vocab, int64_t* __restrict__ out) {
+  constexpr int64_t NT = 1024;  // threads per workgroup
   __shared__ float sv[16];
   __shared__ int64_t si[16];
   const int64_t row = blockIdx.x;
@@ -185,16 +194,16 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const uint16_t* __restrict
   if (((uintptr_t)lr & 15) == 0) {
     const int64_t nch = vocab >> 3;
     const u32x4* lc = reinterpret_cast<const u32x4*>(lr);
-    for (int64_t c0 = threadIdx.x; c0 < nch; c0 += 4 * (int64_t)blockDim.x) {
+    for (int64_t c0 = threadIdx.x; c0 < nch; c0 += 4 * NT) {
       u32x4 v[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const int64_t c = c0 + u * (int64_t)blockDim.x;
+        const int64_t c = c0 + u * NT;
         v[u] = lc[c < nch ? c : nch - 1];
       }
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const int64_t c = c0 + u * (int64_t)blockDim.x;
+        const int64_t c = c0 + u * NT;
         if (c >= nch) continue;
         const uint32_t w[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
 #pragma unroll
@@ -209,7 +218,7 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const uint16_t* __restrict
     }
     done = nch << 3;
   }
-  for (int64_t i = done + threadIdx.x; i < vocab; i += blockDim.x) {
+  for (int64_t i = done + threadIdx.x; i < vocab; i += NT) {
     const float v = bf16_bits_to_f32(lr[i]);
     if (better(v, i, bv, bi)) {
       bv = v;
@@ -232,14 +241,14 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const uint16_t* __restrict
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    const int nw = blockDim.x >> 6;
-    for (int wv = 1; wv < nw; ++wv)
+    for (int wv = 1; wv < (int)(NT >> 6); ++wv)
       if (better(sv[wv], si[wv], bv, bi)) {
         bv = sv[wv];
         bi = si[wv];
       }
-    out[row] = bi == INT64_MAX ? 0 : bi;
+    st_agent(out + row, bi == INT64_MAX ? (int64_t)0 : bi);
   }
+  stores_done();
 }
 
 // One workgroup of 1024 threads per row.  With argmax_keys, the row's next
@@ -259,7 +268,8 @@ __global__ __launch_bounds__(1024) void decode_advance_kernel(
     int64_t* ids, int64_t* positions, int32_t* seq_lens, int64_t* slot_mapping,
     const int32_t* block_table, int64_t* tokens_out, int max_blocks, int block_size,
     int max_len, const uint16_t* __restrict__ embed_table, uint16_t* __restrict__ embed_out,
-    int64_t vocab, int64_t hidden) {
+    int64_t vocab, int64_t hidden, int nt) {
+  // nt = the workgroup size: 1024 with argmax keys or an embedding, else 64
   constexpr int KPT = 16;  // keys per thread per round trip
   __shared__ uint64_t red[16];
   __shared__ int64_t s_nid;
@@ -301,17 +311,17 @@ __global__ __launch_bounds__(1024) void decode_advance_kernel(
   if (tid == 0) {
     int64_t argmax_id = nxt0;
     if (argmax_keys) {
-      for (int i = 1; i < (int)(blockDim.x >> 6); ++i) key = red[i] > key ? red[i] : key;
+      for (int i = 1; i < (nt >> 6); ++i) key = red[i] > key ? red[i] : key;
       argmax_id = key ? (int64_t)(0xffffffffu - (uint32_t)key) : 0;
-      next_ids[r] = argmax_id;
+      st_agent(next_ids + r, argmax_id);
     }
     const int64_t nid = (forced_ids && p < flen && p < max_len) ? fid : argmax_id;
-    ids[r] = nid;
-    positions[r] = p;
-    seq_lens[r] = (int32_t)(p + 1);
-    slot_mapping[r] =
-        p / block_size < max_blocks ? (int64_t)bte * block_size + p % block_size : -1;
-    if (tokens_out && p < max_len) tokens_out[(int64_t)r * max_len + p] = nid;
+    st_agent(ids + r, nid);
+    st_agent(positions + r, p);
+    st_agent(seq_lens + r, (int32_t)(p + 1));
+    st_agent(slot_mapping + r,
+             p / block_size < max_blocks ? (int64_t)bte * block_size + p % block_size : (int64_t)-1);
+    if (tokens_out && p < max_len) st_agent(tokens_out + (int64_t)r * max_len + p, nid);
     s_nid = nid;
   }
   if (embed_table) {
@@ -319,9 +329,10 @@ __global__ __launch_bounds__(1024) void decode_advance_kernel(
     const int64_t nid = s_nid;
     const bool ok = nid >= 0 && nid < vocab;
     const uint16_t* src = embed_table + (ok ? nid : 0) * hidden;
-    for (int64_t i = tid; i < hidden; i += blockDim.x)
-      embed_out[(int64_t)r * hidden + i] = ok ? src[i] : (uint16_t)0;
+    for (int64_t i = tid; i < hidden; i += nt)
+      st_agent(embed_out + (int64_t)r * hidden + i, ok ? src[i] : (uint16_t)0);
   }
+  stores_done();
 }
 
 // One wave per (kv head, token): copies head_dim bf16 of K and of V.
@@ -335,9 +346,10 @@ __global__ __launch_bounds__(64) void reshape_and_cache_kernel(
   const int64_t src = ((int64_t)t * n_kv + h) * head_dim;
   const int64_t dst = (slot * n_kv + h) * head_dim;
   for (int i = threadIdx.x; i < head_dim; i += 64) {
-    k_cache[dst + i] = key[src + i];
-    v_cache[dst + i] = value[src + i];
+    st_agent(k_cache + dst + i, key[src + i]);
+    st_agent(v_cache + dst + i, value[src + i]);
   }
+  stores_done();
 }
 
 // Slot of every token of a (ragged) batch: token t of request r (the r with
@@ -366,7 +378,8 @@ __global__ __launch_bounds__(256) void slot_mapping_kernel(
         v = (int64_t)block_table[(int64_t)lo * max_blocks + blk] * block_size + pos % block_size;
     }
   }
-  out[t] = v;
+  st_agent(out + t, v);
+  stores_done();
 }
 
 }  // namespace
@@ -392,9 +405,9 @@ extern "C" int smx_add_rmsnorm(void* stream, const void* x, const void* residual
                                             : smx::add_rmsnorm_kernel<1, false>)
                                 : (residual ? smx::add_rmsnorm_kernel<2, true>
                                             : smx::add_rmsnorm_kernel<2, false>);
-  hipLaunchKernelGGL(kern, dim3((unsigned)rows), dim3(threads), 0, (hipStream_t)stream,
+  SMX_LAUNCH(kern, dim3((unsigned)rows), dim3(threads), 0, (hipStream_t)stream,
                      (const uint16_t*)x, (const uint16_t*)residual, (const uint16_t*)gamma,
-                     (uint16_t*)y, (uint16_t*)residual_out, (int)hidden, eps);
+                     (uint16_t*)y, (uint16_t*)residual_out, (int)hidden, eps, threads);
   return (int)hipGetLastError();
 }
 
@@ -416,7 +429,7 @@ extern "C" int smx_qknorm_rope_kv_write(void* stream, const void* qkv, const voi
   SMX_REQUIRE(eps >= 0.f && isfinite(eps), "eps must be finite and >= 0");
   SMX_REQUIRE((uintptr_t)positions % 8 == 0 && (uintptr_t)slot_mapping % 8 == 0,
               "int64 arrays must be 8-byte aligned");
-  hipLaunchKernelGGL(smx::qknorm_rope_kv_kernel, dim3(n_q + 2 * n_kv, num_tokens), dim3(64), 0,
+  SMX_LAUNCH(smx::qknorm_rope_kv_kernel, dim3(n_q + 2 * n_kv, num_tokens), dim3(64), 0,
                      (hipStream_t)stream, (const uint16_t*)qkv, (const uint16_t*)q_gamma,
                      (const uint16_t*)k_gamma, (const uint16_t*)cos_sin, positions, slot_mapping,
                      (uint16_t*)q_out, (uint16_t*)k_cache, (uint16_t*)v_cache, n_q, n_kv,
@@ -430,7 +443,7 @@ extern "C" int smx_silu_mul(void* stream, const void* gate_up, void* out, int64_
   SMX_REQUIRE(rows >= 1 && d >= 1 && rows * d < (1ll << 40), "bad shape");
   const int64_t grid = (rows * d + 255) / 256;
   SMX_REQUIRE(grid < (1ll << 31), "tensor too large");
-  hipLaunchKernelGGL(smx::silu_mul_kernel, dim3((unsigned)grid), dim3(256), 0,
+  SMX_LAUNCH(smx::silu_mul_kernel, dim3((unsigned)grid), dim3(256), 0,
                      (hipStream_t)stream, (const uint16_t*)gate_up, (uint16_t*)out, rows, d);
   return (int)hipGetLastError();
 }
@@ -442,9 +455,9 @@ extern "C" int smx_embedding(void* stream, const void* table, const int64_t* ids
   SMX_REQUIRE(vocab >= 1 && hidden >= 1, "vocab and hidden must be >= 1");
   SMX_REQUIRE((uintptr_t)ids % 8 == 0, "ids must be 8-byte aligned");
   const unsigned gx = (unsigned)((hidden + 255) / 256 < 64 ? (hidden + 255) / 256 : 64);
-  hipLaunchKernelGGL(smx::embedding_kernel, dim3(gx, (unsigned)num_tokens), dim3(256), 0,
+  SMX_LAUNCH(smx::embedding_kernel, dim3(gx, (unsigned)num_tokens), dim3(256), 0,
                      (hipStream_t)stream, (const uint16_t*)table, ids, (uint16_t*)out, vocab,
-                     hidden);
+                     hidden, (int)gx);
   return (int)hipGetLastError();
 }
 
@@ -453,7 +466,7 @@ extern "C" int smx_argmax_bf16(void* stream, const void* logits, int64_t rows, i
   SMX_REQUIRE(logits && out_ids, "null pointer argument");
   SMX_REQUIRE(rows >= 1 && rows < (1ll << 31) && vocab >= 1, "bad shape");
   SMX_REQUIRE((uintptr_t)out_ids % 8 == 0, "out_ids must be 8-byte aligned");
-  hipLaunchKernelGGL(smx::argmax_kernel, dim3((unsigned)rows), dim3(1024), 0,
+  SMX_LAUNCH(smx::argmax_kernel, dim3((unsigned)rows), dim3(1024), 0,
                      (hipStream_t)stream, (const uint16_t*)logits, vocab, out_ids);
   return (int)hipGetLastError();
 }
@@ -467,7 +480,7 @@ extern "C" int smx_reshape_and_cache(void* stream, const void* key, const void* 
   SMX_REQUIRE(n_kv >= 1 && n_kv <= 65535 && head_dim >= 1 && head_dim <= 4096, "bad head shape");
   SMX_REQUIRE(num_blocks >= 1 && block_size >= 1, "num_blocks and block_size must be >= 1");
   SMX_REQUIRE((uintptr_t)slot_mapping % 8 == 0, "slot_mapping must be 8-byte aligned");
-  hipLaunchKernelGGL(smx::reshape_and_cache_kernel, dim3(n_kv, num_tokens), dim3(64), 0,
+  SMX_LAUNCH(smx::reshape_and_cache_kernel, dim3(n_kv, num_tokens), dim3(64), 0,
                      (hipStream_t)stream, (const uint16_t*)key, (const uint16_t*)value,
                      (uint16_t*)k_cache, (uint16_t*)v_cache, slot_mapping, n_kv, head_dim,
                      (int64_t)num_blocks * block_size);
@@ -496,11 +509,11 @@ extern "C" int smx_decode_advance(void* stream, int64_t* next_ids, const uint64_
   SMX_REQUIRE(!embed_table || (vocab >= 1 && hidden >= 1 && (uintptr_t)embed_table % 2 == 0 &&
                                (uintptr_t)embed_out % 2 == 0),
               "embedding needs vocab, hidden >= 1 and 2-byte aligned tables");
-  hipLaunchKernelGGL(smx::decode_advance_kernel, dim3(rows),
-                     dim3(argmax_keys || embed_table ? 1024 : 64), 0, (hipStream_t)stream,
-                     next_ids, argmax_keys, num_keys, forced_ids, forced_len, ids, positions,
-                     seq_lens, slot_mapping, block_table, tokens_out, max_blocks, block_size,
-                     max_len, (const uint16_t*)embed_table, (uint16_t*)embed_out, vocab, hidden);
+  const int nt = argmax_keys || embed_table ? 1024 : 64;
+  SMX_LAUNCH(smx::decode_advance_kernel, dim3(rows), dim3(nt), 0, (hipStream_t)stream,
+             next_ids, argmax_keys, num_keys, forced_ids, forced_len, ids, positions, seq_lens,
+             slot_mapping, block_table, tokens_out, max_blocks, block_size, max_len,
+             (const uint16_t*)embed_table, (uint16_t*)embed_out, vocab, hidden, nt);
   return (int)hipGetLastError();
 }
 extern "C" int smx_compute_slot_mapping(void* stream, const int32_t* query_start_loc,
@@ -517,7 +530,7 @@ extern "C" int smx_compute_slot_mapping(void* stream, const int32_t* query_start
   SMX_REQUIRE((uintptr_t)positions % 8 == 0 && (uintptr_t)slot_mapping % 8 == 0 &&
                   (uintptr_t)query_start_loc % 4 == 0 && (uintptr_t)block_table % 4 == 0,
               "misaligned pointer");
-  hipLaunchKernelGGL(smx::slot_mapping_kernel, dim3((max_tokens + 255) / 256), dim3(256), 0,
+  SMX_LAUNCH(smx::slot_mapping_kernel, dim3((max_tokens + 255) / 256), dim3(256), 0,
                      (hipStream_t)stream, query_start_loc, num_reqs, positions, block_table,
                      slot_mapping, num_tokens, max_tokens, max_blocks, block_size);
   return (int)hipGetLastError();

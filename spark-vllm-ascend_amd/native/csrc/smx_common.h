@@ -24,6 +24,32 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
+// Stores of values that another kernel reads.  They are agent-scope (sc1)
+// stores: written through this XCD's L2 to the device's coherence point,
+// where a kernel on any XCD that starts after this one has ended reads them,
+// so the boundary between the two kernels needs no L2 write-back (the
+// step runner's acquire-only fence mode relies on it).  Every kernel calls
+// stores_done() after its last such store: its waves end only once the
+// stores have completed.
+template <typename T>
+__device__ __forceinline__ void st_agent(T* p, T v) {
+  static_assert(sizeof(T) == 1 || sizeof(T) == 2 || sizeof(T) == 4 || sizeof(T) == 8,
+                "8- to 64-bit stores");
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(float* p, float v) {
+  st_agent(reinterpret_cast<uint32_t*>(p), __float_as_uint(v));
+}
+__device__ __forceinline__ void st_agent(u32x2* p, u32x2 v) {
+  st_agent(reinterpret_cast<uint64_t*>(p), (uint64_t)v.x | ((uint64_t)v.y << 32));
+}
+__device__ __forceinline__ void st_agent(u32x4* p, u32x4 v) {  // two 64-bit stores
+  uint64_t* q = reinterpret_cast<uint64_t*>(p);
+  st_agent(q, (uint64_t)v.x | ((uint64_t)v.y << 32));
+  st_agent(q + 1, (uint64_t)v.z | ((uint64_t)v.w << 32));
+}
+__device__ __forceinline__ void stores_done() { __builtin_amdgcn_s_waitcnt(0); }
+
 // Unaligned-to-16 (but 4-byte aligned) vector types for the Q4_0 stream:
 // GGUF blocks are 18 bytes, so a block pair starts on a 4-byte boundary only.
 typedef u32x4 u32x4_a4 __attribute__((aligned(4)));

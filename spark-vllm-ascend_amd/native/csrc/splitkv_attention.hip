@@ -24,6 +24,7 @@
 #include <mutex>
 
 #include "smx_common.h"
+#include "smx_launch.h"
 
 namespace smx {
 namespace {
@@ -256,8 +257,9 @@ void splitkv_decode_kernel(
   // comes only now, after the gathered values arrived: the loads above are
   // already in flight, so the branch costs no round trip.
   if (s0 >= s1) {  // uniform over the workgroup
-    for (int i = tid; i < G * HD; i += NT) po[i] = 0.f;
-    if (tid < G) pl[tid] = -INFINITY;
+    for (int i = tid; i < G * HD; i += NT) st_agent(po + i, 0.f);
+    if (tid < G) st_agent(pl + tid, -INFINITY);
+    stores_done();
     return;
   }
   const int w1 = min(s1, w0 + wlen);
@@ -357,10 +359,10 @@ void splitkv_decode_kernel(
       if (slot >= 0 && slot < ((int64_t)num_blocks << bs_log2)) {
         uint16_t* kd = A.kc_w + (slot * n_kv + kvh) * HD;
         uint16_t* vd = A.vc_w + (slot * n_kv + kvh) * HD;
-        kd[lane] = ku;
-        kd[lane + 64] = kv2;
-        vd[lane] = va;
-        vd[lane + 64] = vb;
+        st_agent(kd + lane, ku);
+        st_agent(kd + lane + 64, kv2);
+        st_agent(vd + lane, va);
+        st_agent(vd + lane + 64, vb);
       }
     }
   } else {
@@ -519,11 +521,12 @@ void splitkv_decode_kernel(
       ot += a * o_w[wv][e];
     }
     // lt == 0 only when the split has no token: the empty partial (0, -inf)
-    po[e] = bad ? __builtin_nanf("") : (lt > 0.f ? ot / lt : 0.f);
+    st_agent(po + e, bad ? __builtin_nanf("") : (lt > 0.f ? ot / lt : 0.f));
     if ((e % HD) == 0)
-      pl[h] = bad ? __builtin_nanf("")
-                  : (lt > 0.f ? (mt + log2f(lt)) * 0.69314718055994530942f : -INFINITY);
+      st_agent(pl + h, bad ? __builtin_nanf("")
+                           : (lt > 0.f ? (mt + log2f(lt)) * 0.69314718055994530942f : -INFINITY));
   }
+  stores_done();
 }
 
 // Max / sum over the 64 lanes of a wave (every lane gets the result).
@@ -628,7 +631,8 @@ __global__ __launch_bounds__(64 * MERGE_WAVES) void lse_merge_kernel(
     }
   }
   const float r = poisoned || acc != acc ? __builtin_nanf("") : (l > 0.f ? acc / l : 0.f);
-  out[((int64_t)seq * n_q + h) * HD + d] = f32_to_bf16(r);
+  st_agent(out + ((int64_t)seq * n_q + h) * HD + d, f32_to_bf16(r));
+  stores_done();
 }
 
 
@@ -702,16 +706,17 @@ __global__ __launch_bounds__(64) void splitkv_plan_kernel(
                                   min((tb >> bs_log2) + lane - PLAN_PAGE0, max_blocks - 1)];
       }
     }
-    plan[(int64_t)b * PLAN_WORDS + lane] = w;
+    st_agent(plan + (int64_t)b * PLAN_WORDS + lane, w);
   }
   if (b < num_seqs * num_splits) {
     const int seq = b / num_splits;
     if (b - seq * num_splits >= __shfl(n, seq)) {
-      f32x4* po = reinterpret_cast<f32x4*>(part_o + (int64_t)b * n_q * HD);
-      for (int e = lane; e < n_q * HD / 4; e += 64) po[e] = f32x4{0.f, 0.f, 0.f, 0.f};
-      for (int h = lane; h < n_q; h += 64) part_lse[(int64_t)b * n_q + h] = -INFINITY;
+      u32x4* po = reinterpret_cast<u32x4*>(part_o + (int64_t)b * n_q * HD);
+      for (int e = lane; e < n_q * HD / 4; e += 64) st_agent(po + e, u32x4{0u, 0u, 0u, 0u});
+      for (int h = lane; h < n_q; h += 64) st_agent(part_lse + (int64_t)b * n_q + h, -INFINITY);
     }
   }
+  stores_done();
 }
 
 }  // namespace
@@ -761,19 +766,19 @@ int launch_splitkv(void* stream, smx::SplitKVArgs a, int32_t num_seqs, int32_t b
 #define SMX_ATTN_LAUNCH(W, B)                                                                   \
   do {                                                                                          \
     if (plan && recfast)                                                                        \
-      hipLaunchKernelGGL((smx::splitkv_decode_kernel<W, B, FUSEQ, true, true>), grid,           \
+      SMX_LAUNCH((smx::splitkv_decode_kernel<W, B, FUSEQ, true, true>), grid,           \
                          dim3(64 * W), 0, (hipStream_t)stream, a.block_table, (const void*)plan,  \
                          FUSEQ ? (const void*)a.positions : (const void*)a.kc,                     \
                          FUSEQ ? (const void*)a.slot_mapping : (const void*)a.vc, a.q,             \
                          a.num_splits, a.max_blocks, a.bs_log2, a.n_kv, a);                        \
     else if (plan)                                                                              \
-      hipLaunchKernelGGL((smx::splitkv_decode_kernel<W, B, FUSEQ, true>), grid, dim3(64 * W),   \
+      SMX_LAUNCH((smx::splitkv_decode_kernel<W, B, FUSEQ, true>), grid, dim3(64 * W),   \
                          0, (hipStream_t)stream, a.block_table, (const void*)plan,                \
                          FUSEQ ? (const void*)a.positions : (const void*)a.kc,                     \
                          FUSEQ ? (const void*)a.slot_mapping : (const void*)a.vc, a.q,             \
                          a.num_splits, a.max_blocks, a.bs_log2, a.n_kv, a);                        \
     else                                                                                        \
-      hipLaunchKernelGGL((smx::splitkv_decode_kernel<W, B, FUSEQ, false>), grid, dim3(64 * W),  \
+      SMX_LAUNCH((smx::splitkv_decode_kernel<W, B, FUSEQ, false>), grid, dim3(64 * W),  \
                          0, (hipStream_t)stream, a.block_table, (const void*)a.seq_lens,          \
                          FUSEQ ? (const void*)a.positions : (const void*)a.kc,                     \
                          FUSEQ ? (const void*)a.slot_mapping : (const void*)a.vc, a.q,             \
@@ -821,7 +826,7 @@ int launch_merge(void* stream, const float* partial_o, const float* partial_lse,
                  int32_t num_seqs, int32_t num_splits, int32_t n_q) {
   // one chunk per wave where possible (at most MERGE_WAVES waves)
   const int nw = std::min((num_splits + smx::MCH - 1) / smx::MCH, smx::MERGE_WAVES);
-  hipLaunchKernelGGL(smx::lse_merge_kernel, dim3(2 * n_q, num_seqs), dim3(64 * nw), 0,
+  SMX_LAUNCH(smx::lse_merge_kernel, dim3(2 * n_q, num_seqs), dim3(64 * nw), 0,
                      (hipStream_t)stream, partial_o, partial_lse, (uint16_t*)out, num_splits,
                      n_q, nw);
   return (int)hipGetLastError();
@@ -1039,7 +1044,7 @@ extern "C" int smx_splitkv_plan(void* stream, const int32_t* seq_lens, const int
   int bs_log2 = 0;
   while ((1 << bs_log2) < block_size) ++bs_log2;
   const int64_t grid = std::max<int64_t>(num_items + num_seqs, (int64_t)num_seqs * num_splits);
-  hipLaunchKernelGGL(smx::splitkv_plan_kernel, dim3((unsigned)grid), dim3(64), 0,
+  SMX_LAUNCH(smx::splitkv_plan_kernel, dim3((unsigned)grid), dim3(64), 0,
                      (hipStream_t)stream, seq_lens, positions, slot_mapping, block_table, plan,
                      partial_o, partial_lse, num_seqs, num_items, num_splits, max_blocks, bs_log2,
                      n_q);

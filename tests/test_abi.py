@@ -88,6 +88,13 @@ def test_bindings_cover_header():
      (None, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16, None, 1, 4, 8, 8, 128, 32, 8, 128, 100, 1e-6, 0.1)),
     ("smx_qknorm_rope_splitkv_decode_merged",
      (None, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16, 16, 1, 4, 8, 8, 128, 32, 8, 64, 100, 1e-6, 0.1)),
+    ("smx_runner_create", (None, 0, None)),
+    ("smx_runner_begin", (None,)),
+    ("smx_runner_end", (None,)),
+    ("smx_runner_num_packets", (None, None)),
+    ("smx_runner_replay", (None, 1, 0)),
+    ("smx_runner_wait", (None, 1.0)),
+    ("smx_runner_elapsed", (None, None)),
 ])
 def test_invalid_arguments_rejected_on_host(call, args):
     native = pkg("native")

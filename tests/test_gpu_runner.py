@@ -1,0 +1,153 @@
+"""GPU tests of the step runner (native/runner.py, smx_runner_* in
+include/smx.h): one decode step recorded once and replayed as AQL dispatch
+packets must give eager execution's results bit for bit -- tokens, logits,
+decode state and every KV cache slot -- for the fused and unfused
+one-sequence steps and the batched step, over many steps per replay call and
+over several calls; recording launches nothing; a recording that allocates
+device memory or raises is refused.  (Eager execution is the reference: a
+graph replays it bit for bit too, but capture() runs a warm-up step that
+writes one KV slot outside the sequences' block tables.)"""
+import numpy as np
+import pytest
+
+from _util import bits_of, pkg
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dev():
+    import torch
+    return torch.device("cuda:0")
+
+
+def _m():
+    return pkg("integration.model")
+
+
+def tiny_cfg():
+    return _m().DecoderConfig(hidden=256, n_layers=2, n_q=8, n_kv=2, head_dim=128,
+                              intermediate=512, vocab=1000, block_size=32)
+
+
+def _state_bits(model):
+    st = model.state
+    out = {"tokens": st.tokens.cpu().numpy(), "positions": st.positions.cpu().numpy(),
+           "seq_lens": st.seq_lens.cpu().numpy(), "slots": st.slot_mapping.cpu().numpy(),
+           "logits": bits_of(model.logits), "x": bits_of(model.x)}
+    for i, L in enumerate(model.layers):
+        out[f"k{i}"] = bits_of(L.kv_cache[0])
+        out[f"v{i}"] = bits_of(L.kv_cache[1])
+    return out
+
+
+def _assert_same(a, b, what):
+    assert a.keys() == b.keys()
+    for k in a:
+        np.testing.assert_array_equal(a[k], b[k], err_msg=f"{what}: {k}")
+
+
+def _eager_vs_runner(dev, fences, *, fused=True, batch=1, steps=30, chunks=(30,), seed=5):
+    import torch
+    m = _m()
+    kw = dict(seed=seed, max_len=64, num_splits=2, fused=fused)
+    if batch > 1:
+        kw.update(batch=batch)
+    e = m.DecodeModel(tiny_cfg(), dev, **kw)
+    r = m.DecodeModel(tiny_cfg(), dev, **kw)
+    rng = np.random.default_rng(seed)
+    prompts = [torch.tensor(rng.integers(0, 1000, 3 + i)) for i in range(batch)]
+    prompt = prompts[0] if batch == 1 else prompts
+    e.reset(prompt)
+    for _ in range(steps):
+        e.step()
+    torch.cuda.synchronize()
+    want = _state_bits(e)
+    r.reset(prompt)
+    n = r.record_runner().num_packets
+    assert n > 0
+    assert sum(chunks) == steps
+    for c in chunks:
+        r.run_steps(c, fences)
+    _assert_same(want, _state_bits(r), f"{fences} fences, fused={fused}, batch={batch}")
+    r.runner.close()
+    return n
+
+
+FENCES = ["agent", "acquire"]
+
+
+@pytest.mark.parametrize("fences", FENCES)
+@pytest.mark.parametrize("fused", [True, False])
+def test_runner_replays_the_step(dev, fused, fences):
+    n = _eager_vs_runner(dev, fences, fused=fused)
+    # fused: per layer QKV, attention, merge, o_proj, gate/up, down; head + advance
+    if fused:
+        assert n == 2 * 6 + 2
+
+
+@pytest.mark.parametrize("fences", FENCES)
+def test_runner_batched_step(dev, fences):
+    _eager_vs_runner(dev, fences, batch=3, chunks=(1, 12, 17))
+
+
+@pytest.mark.parametrize("fences", FENCES)
+def test_runner_steps_per_call_do_not_matter(dev, fences):
+    _eager_vs_runner(dev, fences, chunks=(1, 1, 5, 23), seed=6)
+
+
+def test_recording_launches_nothing(dev):
+    import torch
+    m = _m()
+    model = m.DecodeModel(tiny_cfg(), dev, seed=4, max_len=64, num_splits=2)
+    model.reset(torch.tensor([5, 6, 7]))
+    torch.cuda.synchronize()
+    before = _state_bits(model)
+    model.record_runner()
+    torch.cuda.synchronize()
+    _assert_same(before, _state_bits(model), "after recording")
+    model.runner.close()
+
+
+def test_recording_refuses_allocations_and_errors(dev):
+    import torch
+    native = pkg("native")
+    ops = pkg("native.torch_ops")
+    StepRunner = pkg("native.runner").StepRunner
+    x = torch.randn(1, 256, device=dev).to(torch.bfloat16)
+    w = torch.zeros(64, 8 * 18, dtype=torch.uint8, device=dev)
+    with StepRunner() as runner:
+        # an output allocated inside the recording would dangle after it
+        with pytest.raises(RuntimeError, match="allocated"):
+            runner.record(lambda: ops.q4_0_gemv(x, w, 64, 256))
+        with pytest.raises(RuntimeError, match="nothing recorded"):
+            runner.replay(1)
+        # a failing library call stops the recording and propagates
+        with pytest.raises(native.SmxError, match="multiple of 32"):
+            runner.record(lambda: native.call("smx_q4_0_gemv", None, 16, 16, 16, 64, 100))
+        y = torch.empty(1, 64, dtype=torch.bfloat16, device=dev)
+        assert runner.record(lambda: ops.q4_0_gemv(x, w, 64, 256, out=y)) == 1
+        y.fill_(1.0)
+        runner.run(3)
+        assert float(y.float().abs().max()) == 0.0  # zero weights: y = 0
+        runner.wait(1.0)  # idle: returns at once
+
+
+def test_runner_elapsed_is_gpu_time_of_the_last_replay(dev):
+    import time
+    import torch
+    m = _m()
+    model = m.DecodeModel(tiny_cfg(), dev, seed=4, max_len=64, num_splits=2)
+    model.reset(torch.tensor([5, 6, 7]))
+    runner = model.record_runner()
+    with pytest.raises(pkg("native").SmxError, match="nothing replayed"):
+        runner.elapsed()
+    for steps in (1, 40):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        runner.replay(steps, "acquire", sync=False)
+        runner.wait(30.0)
+        wall = time.perf_counter() - t0
+        gpu = runner.elapsed()
+        assert 0.0 < gpu <= wall
+    runner.close()
