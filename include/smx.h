@@ -499,7 +499,8 @@ int smx_runner_wait(smx_runner* runner, double timeout_s);
 /* GPU time of the last replay, from its first kernel's start to its last
  * kernel's end (packet-processor timestamps), once it has completed. */
 int smx_runner_elapsed(smx_runner* runner, double* seconds);
-/* Waits (at most 60 s) for running replays, then frees the runner. */
+/* Waits (at most 60 s) for running replays, then frees the runner (a runner
+ * whose replays do not complete in that time is left allocated). */
 void smx_runner_destroy(smx_runner* runner);
 
 #ifdef __cplusplus
