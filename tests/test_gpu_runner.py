@@ -3,8 +3,9 @@ include/smx.h): one decode step recorded once and replayed as AQL dispatch
 packets must give eager execution's results bit for bit -- tokens, logits,
 decode state and every KV cache slot -- for the fused and unfused
 one-sequence steps and the batched step, over many steps per replay call and
-over several calls; recording launches nothing; a recording that allocates
-device memory or raises is refused.  (Eager execution is the reference: a
+over several calls, and the 36-layer 4B-shape model at contexts near 4000
+(one sequence and eight); recording launches nothing; a recording that
+allocates device memory or raises is refused.  (Eager execution is the reference: a
 graph replays it bit for bit too, but capture() runs a warm-up step that
 writes one KV slot outside the sequences' block tables.)"""
 import numpy as np
@@ -151,3 +152,39 @@ def test_runner_elapsed_is_gpu_time_of_the_last_replay(dev):
         gpu = runner.elapsed()
         assert 0.0 < gpu <= wall
     runner.close()
+
+
+@pytest.mark.parametrize("batch", [1, 8])
+def test_runner_4b_model_matches_eager(dev, batch):
+    """The 36-layer 4B-shape model at real kernel shapes (49 capacity splits
+    for one sequence; the per-sequence plan, MFMA GEMMs and the batched head
+    for 8): 6 steps from contexts near 4000 through the runner (acquire-only
+    fences) equal 6 eager steps bit for bit -- tokens, logits, decode state
+    and the K/V slots the steps wrote."""
+    import torch
+    m = _m()
+    model = m.DecodeModel(m.DecoderConfig(), dev, seed=2, max_len=6272, batch=batch)
+    model.fill_kv(21)
+    ctx = [4000 + 97 * r for r in range(batch)]
+    ids = [1 + 13 * r for r in range(batch)]
+    steps = 6
+
+    def run(step_fn):
+        model.set_context(ctx, ids=ids)
+        step_fn()
+        torch.cuda.synchronize()
+        st = model.state
+        bs = model.cfg.block_size
+        slots = [int(st.block_table[r, p // bs]) * bs + p % bs
+                 for r in range(batch) for p in range(ctx[r], ctx[r] + steps)]
+        idx = torch.tensor(slots, device=dev)
+        kv = [bits_of(L.kv_cache.flatten(1, 2)[:, idx]) for L in model.layers]
+        return {"tokens": st.tokens.cpu().numpy(), "positions": st.positions.cpu().numpy(),
+                "slots": st.slot_mapping.cpu().numpy(), "logits": bits_of(model.logits),
+                "x": bits_of(model.x), **{f"kv{i}": a for i, a in enumerate(kv)}}
+
+    want = run(lambda: [model.step() for _ in range(steps)])
+    model.record_runner()
+    got = run(lambda: model.run_steps(steps, "acquire"))
+    model.runner.close()
+    _assert_same(want, got, f"4B model, batch {batch}")
