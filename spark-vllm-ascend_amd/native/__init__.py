@@ -110,6 +110,27 @@ def library_sha256(path: Path = LIB_PATH) -> str:
     return hashlib.sha256(Path(path).read_bytes()).hexdigest()
 
 
+def _file_sha256(path) -> str:
+    return hashlib.sha256(Path(path).read_bytes()).hexdigest()
+
+
+def check_code_objects(record_path, paths) -> None:
+    """Raise RuntimeError unless the validation record at record_path holds
+    the sha256 of every device code object in paths: the step runner loads
+    them beside the library, so the record vouches for them too."""
+    try:
+        rec = json.loads(Path(record_path).read_text())
+    except (OSError, ValueError) as exc:
+        raise RuntimeError(f"validation record {record_path} unreadable: {exc}") from exc
+    want = rec.get("code_objects_sha256") if isinstance(rec, dict) else None
+    want = want if isinstance(want, dict) else {}
+    bad = [Path(p).name for p in paths
+           if not Path(p).exists() or want.get(Path(p).name) != _file_sha256(p)]
+    if bad:
+        raise RuntimeError(f"validation record {record_path} rejected: code objects {bad} "
+                           "are not the ones it validated")
+
+
 def check_validation_record(record_path, lib_path: Path = LIB_PATH) -> str:
     """Raise RuntimeError unless the JSON validation record at record_path
     vouches for the library at lib_path: a complete GPU test run of this ABI

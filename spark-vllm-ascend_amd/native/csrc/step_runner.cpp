@@ -23,6 +23,7 @@
 #include <iterator>
 #include <string>
 #include <unordered_map>
+#include <unordered_set>
 #include <vector>
 
 #include "../../../include/smx.h"
@@ -115,6 +116,7 @@ hsa_status_t visit_gpu_pool(hsa_amd_memory_pool_t pool, void* data) {
 struct SymbolScan {
   hsa_executable_t exe;
   std::unordered_map<std::string, KernelInfo>* out;
+  std::unordered_set<std::string>* ambiguous;  // names found in more than one code object
 };
 
 hsa_status_t visit_symbol(hsa_executable_t, hsa_agent_t, hsa_executable_symbol_t sym, void* data) {
@@ -138,7 +140,7 @@ hsa_status_t visit_symbol(hsa_executable_t, hsa_agent_t, hsa_executable_symbol_t
                                  &k.group_size);
   hsa_executable_symbol_get_info(sym, HSA_EXECUTABLE_SYMBOL_INFO_KERNEL_PRIVATE_SEGMENT_SIZE,
                                  &k.private_size);
-  (*s->out)[name] = k;
+  if (!s->out->emplace(name, k).second) s->ambiguous->insert(name);
   return HSA_STATUS_SUCCESS;
 }
 
@@ -158,6 +160,7 @@ struct smx_runner final : smx::LaunchSink {
   std::vector<hsa_code_object_reader_t> readers;
   std::vector<hsa_executable_t> executables;
   std::unordered_map<std::string, KernelInfo> kernels;
+  std::unordered_set<std::string> ambiguous;
   hsa_queue_t* queue = nullptr;
   hsa_signal_t pending{0};  // decremented by the last packet of each replay
   hsa_signal_t first{0};    // completion signal of the first packet (timing)
@@ -185,6 +188,10 @@ struct smx_runner final : smx::LaunchSink {
     auto it = kernels.find(name);
     if (it == kernels.end()) {
       record_error = std::string("kernel not in the runner's code objects: ") + name;
+      return;
+    }
+    if (ambiguous.count(name)) {
+      record_error = std::string("kernel defined in more than one code object: ") + name;
       return;
     }
     const KernelInfo& k = it->second;
@@ -300,7 +307,7 @@ extern "C" int smx_runner_create(const char* const* code_objects, int32_t count,
             HSA_STATUS_SUCCESS ||
         hsa_executable_freeze(exe, nullptr) != HSA_STATUS_SUCCESS)
       return bail(std::string("cannot load ") + code_objects[i]);
-    SymbolScan scan{exe, &r->kernels};
+    SymbolScan scan{exe, &r->kernels, &r->ambiguous};
     if (hsa_executable_iterate_agent_symbols(exe, r->gpu, visit_symbol, &scan) !=
         HSA_STATUS_SUCCESS)
       return bail("cannot list kernels");

@@ -23,10 +23,12 @@ recording time instead.
 from __future__ import annotations
 
 import ctypes
+import os
 
 import torch
 
-from . import RUNNER_FENCES_ACQUIRE_ONLY, RUNNER_FENCES_AGENT, SmxError, call, load
+from . import (RUNNER_FENCES_ACQUIRE_ONLY, RUNNER_FENCES_AGENT, VALIDATION_ENV, SmxError, call,
+               check_code_objects, load)
 from .build import code_object_paths
 
 FENCES = {"agent": RUNNER_FENCES_AGENT, "acquire": RUNNER_FENCES_ACQUIRE_ONLY}
@@ -47,6 +49,9 @@ class StepRunner:
         if missing:
             raise RuntimeError(f"device code objects not built: {missing}; run "
                                "__graft_entry__.build()")
+        record = os.environ.get(VALIDATION_ENV)
+        if record:  # the record that vouched for the library vouches for these
+            check_code_objects(record, paths)
         arr = (ctypes.c_char_p * len(paths))(*[str(p).encode() for p in paths])
         handle = ctypes.c_void_p()
         call("smx_runner_create", arr, len(paths), ctypes.byref(handle))

@@ -4,12 +4,14 @@ Runs the repository's GPU test suite (``pytest tests -m gpu``) against the
 library as built, and on completion writes a JSON record
 
   {"complete": true, "library": "libsmx.so", "library_sha256": "...",
+   "code_objects_sha256": {"libsmx.<source>.co": "...", ...},
    "abi_version": N, "pytest": {"exit": 0, "passed": P, "failed": 0,
    "errors": 0, "skipped": S}, "created": "..."}
 
 which ``native.load()`` checks before loading the library whenever the
 environment variable SMX_VALIDATION_RECORD names it (check_validation_record:
-complete, this ABI version, no failure, the library's sha256).  The
+complete, this ABI version, no failure, the library's sha256), and the step
+runner before it loads the device code objects (check_code_objects).  The
 reference deploys its kernel library the same way: a validation run writes
 head-validation.json with the library's digest, and the loader refuses the
 library unless the record is complete and the digest matches
@@ -55,10 +57,19 @@ def _junit_counts(path: Path) -> dict:
     return c
 
 
-def make_record(pytest_exit: int, counts: dict, lib: Path = LIB) -> dict:
+def make_record(pytest_exit: int, counts: dict, lib: Path = LIB, code_objects=None) -> dict:
     import hashlib
+    if code_objects is None:
+        sys.path.insert(0, str(HERE))
+        try:
+            from build import code_object_paths
+        finally:
+            sys.path.pop(0)
+        code_objects = [p for p in code_object_paths() if p.exists()]
     return {"complete": True, "library": lib.name,
             "library_sha256": hashlib.sha256(lib.read_bytes()).hexdigest(),
+            "code_objects_sha256": {Path(p).name: hashlib.sha256(Path(p).read_bytes()).hexdigest()
+                                    for p in code_objects},
             "abi_version": _abi_version(),
             "pytest": {"exit": int(pytest_exit), "passed": counts["passed"],
                        "failed": counts["failed"], "errors": counts["errors"],

@@ -86,3 +86,31 @@ def test_load_is_gated_by_the_environment(tmp_path, good):
         assert res.returncode == 0 and "loaded" in res.stdout, res.stderr
     else:
         assert res.returncode != 0 and "rejected" in res.stderr
+
+
+def test_record_vouches_for_the_runner_code_objects(tmp_path):
+    """The step runner loads the device code objects beside the library: the
+    record carries their digests, and a changed or missing one is refused."""
+    native = pkg("native")
+    paths = [tmp_path / "libsmx.a.co", tmp_path / "libsmx.b.co"]
+    for i, p in enumerate(paths):
+        p.write_bytes(bytes([i]) * 64)
+    validate = pkg("native.validate")
+    rec = validate.make_record(0, {"passed": 1, "failed": 0, "errors": 0, "skipped": 0},
+                               native.LIB_PATH, code_objects=paths)
+    path = tmp_path / "validation.json"
+    path.write_text(json.dumps(rec))
+    native.check_code_objects(path, paths)
+    paths[1].write_bytes(b"\1" * 65)
+    with pytest.raises(RuntimeError, match="libsmx.b.co"):
+        native.check_code_objects(path, paths)
+    with pytest.raises(RuntimeError, match="libsmx.c.co"):
+        native.check_code_objects(path, [paths[0], tmp_path / "libsmx.c.co"])
+
+
+def test_default_record_lists_the_built_code_objects(tmp_path):
+    native = pkg("native")
+    build = pkg("native.build")
+    rec = pkg("native.validate").make_record(
+        0, {"passed": 1, "failed": 0, "errors": 0, "skipped": 0}, native.LIB_PATH)
+    assert set(rec["code_objects_sha256"]) == {p.name for p in build.code_object_paths()}
