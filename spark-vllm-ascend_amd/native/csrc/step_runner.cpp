@@ -157,6 +157,10 @@ void queue_error(hsa_status_t status, hsa_queue_t*, void*) {
 struct smx_runner final : smx::LaunchSink {
   hsa_agent_t gpu{0};
   FindPools pools;
+  // the code objects' bytes stay alive with the runner: the loader (and the
+  // tools that inspect loaded code objects) may refer to the memory they
+  // were loaded from
+  std::vector<std::vector<char>> blobs;
   std::vector<hsa_code_object_reader_t> readers;
   std::vector<hsa_executable_t> executables;
   std::unordered_map<std::string, KernelInfo> kernels;
@@ -291,7 +295,8 @@ extern "C" int smx_runner_create(const char* const* code_objects, int32_t count,
   for (int i = 0; i < count; ++i) {
     if (!code_objects[i]) return bail("null code object path");
     std::ifstream f(code_objects[i], std::ios::binary);
-    std::vector<char> blob((std::istreambuf_iterator<char>(f)), std::istreambuf_iterator<char>());
+    r->blobs.emplace_back((std::istreambuf_iterator<char>(f)), std::istreambuf_iterator<char>());
+    const std::vector<char>& blob = r->blobs.back();
     if (blob.empty()) return bail(std::string("cannot read ") + code_objects[i]);
     hsa_code_object_reader_t reader;
     if (hsa_code_object_reader_create_from_memory(blob.data(), blob.size(), &reader) !=
