@@ -188,3 +188,40 @@ def test_runner_4b_model_matches_eager(dev, batch):
     got = run(lambda: model.run_steps(steps, "acquire"))
     model.runner.close()
     _assert_same(want, got, f"4B model, batch {batch}")
+
+
+def test_recording_is_per_thread(dev):
+    """While one thread records, a library call on another thread launches
+    as usual (the recording runner is the calling thread's)."""
+    import threading
+    import torch
+    native = pkg("native")
+    ops = pkg("native.torch_ops")
+    StepRunner = pkg("native.runner").StepRunner
+    x = torch.randn(1, 256, device=dev).to(torch.bfloat16)
+    w = torch.zeros(64, 8 * 18, dtype=torch.uint8, device=dev)
+    y_rec = torch.full((1, 64), 1.0, dtype=torch.bfloat16, device=dev)
+    y_other = torch.full((1, 64), 1.0, dtype=torch.bfloat16, device=dev)
+    inside, done = threading.Event(), threading.Event()
+
+    def other():
+        inside.wait(30)
+        ops.q4_0_gemv(x, w, 64, 256, out=y_other)  # launched now, on this thread's stream
+        torch.cuda.synchronize()
+        done.set()
+
+    t = threading.Thread(target=other)
+    t.start()
+    with StepRunner() as runner:
+        def fn():
+            ops.q4_0_gemv(x, w, 64, 256, out=y_rec)
+            inside.set()
+            assert done.wait(30)
+        assert runner.record(fn) == 1
+        t.join(30)
+        torch.cuda.synchronize()
+        assert float(y_other.float().abs().max()) == 0.0  # the other thread's GEMV ran
+        assert float(y_rec.float().min()) == 1.0  # the recorded one did not
+        runner.run(1)
+        assert float(y_rec.float().abs().max()) == 0.0
+    assert native.load() is not None
