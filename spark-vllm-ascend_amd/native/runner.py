@@ -16,7 +16,9 @@ Recording launches nothing.  The recorded packets keep raw device pointers,
 so every tensor the recorded calls name must stay alive (and in place) for
 as long as the runner replays them; ``record`` refuses a function that
 allocated device memory while it recorded (a temporary freed afterwards
-would leave a dangling pointer in the packets).  Only this library's calls
+would leave a dangling pointer in the packets; the allocation count it
+checks is the process's, so another thread allocating meanwhile also makes
+it refuse).  Only this library's calls
 are recorded: a torch operation inside the recorded function would run at
 recording time instead.
 """
