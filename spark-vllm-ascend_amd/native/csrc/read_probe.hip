@@ -26,8 +26,10 @@ __global__ __launch_bounds__(256) void read_probe_kernel(const u32x4* __restrict
   for (int i = 0; i < LOADS; ++i) x ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) x ^= (uint32_t)__shfl_xor((int)x, o, 64);
-  if ((threadIdx.x & 63) == 0) st_agent(sink + blockIdx.x * 4 + (threadIdx.x >> 6), x);  // lane 0 of each wave
-  stores_done();
+  // lane 0 of each wave.  A plain store: only the host reads the sink (no
+  // later kernel does), and an agent-scope store would make every wave wait
+  // for its write-through before ending, which the instrument must not time.
+  if ((threadIdx.x & 63) == 0) sink[blockIdx.x * 4 + (threadIdx.x >> 6)] = x;
 }
 
 }  // namespace
