@@ -411,17 +411,23 @@ class DecodeModel:
                                      dtype=torch.int64))
         self.head.embed(st.ids, out=self.x)
 
-    def generate(self, prompt, new_tokens: int) -> torch.Tensor:
+    def generate(self, prompt, new_tokens: int, fences: str | None = None) -> torch.Tensor:
         """Greedy decode: feeds the prompt(s), then new_tokens generated
         tokens.  Returns the token ids by position (prompt followed by
-        generated): [total] for batch 1, else [batch, longest total]."""
+        generated): [total] for batch 1, else [batch, longest total].  With
+        fences, the steps run on the recorded step runner (record_runner)
+        with that fence mode, all of them in one replay."""
         prompts = list(prompt) if isinstance(prompt, (list, tuple)) else [prompt] * self.batch
         total = max(int(torch.as_tensor(p).numel()) for p in prompts) + new_tokens
         if total > self.max_len:
             raise ValueError("prompt + new_tokens exceeds max_len")
         self.reset(prompt)
-        for _ in range(total - 1):
-            self.step()
+        if fences is not None:
+            if total > 1:
+                self.run_steps(total - 1, fences)
+        else:
+            for _ in range(total - 1):
+                self.step()
         torch.cuda.synchronize(self.device)
         out = self.state.tokens[:, :total].clone()
         return out[0] if self.batch == 1 else out

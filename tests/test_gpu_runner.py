@@ -225,3 +225,24 @@ def test_recording_is_per_thread(dev):
         runner.run(1)
         assert float(y_rec.float().abs().max()) == 0.0
     assert native.load() is not None
+
+
+def test_generate_on_the_runner(dev):
+    """generate() through the runner (one replay for prompt + new tokens)
+    returns the graph's tokens, for one sequence and for three ragged ones."""
+    import torch
+    m = _m()
+    rng = np.random.default_rng(17)
+    for batch in (1, 3):
+        kw = dict(seed=9, max_len=64, num_splits=2) if batch == 1 else \
+            dict(seed=9, max_len=64, batch=batch)
+        g = m.DecodeModel(tiny_cfg(), dev, **kw)
+        r = m.DecodeModel(tiny_cfg(), dev, **kw)
+        prompts = [torch.tensor(rng.integers(0, 1000, 4 + 2 * i)) for i in range(batch)]
+        prompt = prompts[0] if batch == 1 else prompts
+        g.capture()
+        want = g.generate(prompt, 20).cpu().numpy()
+        r.record_runner()
+        got = r.generate(prompt, 20, fences="acquire").cpu().numpy()
+        r.runner.close()
+        np.testing.assert_array_equal(want, got, err_msg=f"batch {batch}")
