@@ -8,14 +8,19 @@ whatever --steps is, so the kernels' split count does not follow the run's
 length).  TPOT is the reference's: time per generated token after the first
 ((t_last - t_first) / 4095, src/tools/benchmark/benchmark.py:123).
   --steps 4095 (the default): the protocol itself -- a 2048-token random
-      prompt fed through the captured decode graph, the first generated token
-      untimed, the next 4095 timed.
+      prompt fed through the decode step, the first generated token untimed,
+      the next 4095 timed.
   --steps K < 4095: K timed tokens spread over the protocol's contexts --
       up to 4 segments starting at contexts from 2049 to 6144 - K/4, each
       after --warmup untimed tokens, over a KV cache pre-filled with seeded
       random bf16 -- so a short run reports the protocol's mean context, not
       its first tokens.
-The median over --runs independent runs is reported.
+The median over --runs independent runs is reported.  The steps run on the
+library's step runner (the recorded step replayed as AQL packets on its own
+HSA queue, agent-scope acquire and no release between kernels), timed by the
+GPU's packet-processor timestamps; the same steps then run once through the
+captured graph (graph_ms_per_step, with a token comparison).  Without a
+runner (no HSA queue) the graph is timed instead, with HIP events.
 
 Also reported, on the same box in the same run:
   roofline      the Q4_0 GEMV [9728 x 2560] (the dominant kernel class:
