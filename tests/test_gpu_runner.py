@@ -158,8 +158,8 @@ def test_runner_elapsed_is_gpu_time_of_the_last_replay(dev):
 def test_runner_4b_model_matches_eager(dev, batch):
     """The 36-layer 4B-shape model at real kernel shapes (49 capacity splits
     for one sequence; the per-sequence plan, MFMA GEMMs and the batched head
-    for 8): 6 steps from contexts near 4000 through the runner (acquire-only
-    fences) equal 6 eager steps bit for bit -- tokens, logits, decode state
+    for 8): 6 steps from contexts near 4000 through the runner (either fence
+    mode) equal 6 eager steps bit for bit -- tokens, logits, decode state
     and the K/V slots the steps wrote."""
     import torch
     m = _m()
@@ -185,9 +185,10 @@ def test_runner_4b_model_matches_eager(dev, batch):
 
     want = run(lambda: [model.step() for _ in range(steps)])
     model.record_runner()
-    got = run(lambda: model.run_steps(steps, "acquire"))
+    for fences in FENCES:
+        got = run(lambda: model.run_steps(steps, fences))
+        _assert_same(want, got, f"4B model, batch {batch}, {fences} fences")
     model.runner.close()
-    _assert_same(want, got, f"4B model, batch {batch}")
 
 
 def test_recording_is_per_thread(dev):
