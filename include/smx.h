@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define SMX_ABI_VERSION 7
+#define SMX_ABI_VERSION 8
 
 /* Return codes besides 0 and hipError_t values. */
 #define SMX_EINVAL 10001      /* an argument failed validation */
@@ -86,6 +86,28 @@ int smx_q4_0_gemv_swiglu(void* stream, const void* x, const void* w,
                          void* out, int64_t d, int64_t k);
 
 /*
+ * The reference model's gate/up activation, erf-GELU through a bf16 table
+ * (activate_native, src/spark_vllm_ascend/kernels/linear.py:540-577; the
+ * table is built at src/spark_vllm_ascend/integration/model.py:13-16).
+ * lut[SMX_GELU_LUT_ENTRIES] bf16: lut[i] = RNE_bf16(gelu(b)) for the bf16
+ * bit patterns b = 0x3b00 + i (i < 2048) and b = 0xbb00 + (i - 2048) (i >=
+ * 2048), gelu(x) = x * (1 + erf(x / sqrt(2))) / 2.  For the bf16 gate g:
+ *   act(g) = NaN 0x7fff            g NaN or -inf
+ *            g (+inf included)     g >= 128
+ *            -0                    g <= -128
+ *            RNE_bf16(g / 2)       |g| < 2^-9
+ *            lut[index of g]       otherwise
+ * and the output is RNE_bf16(act(g) * u).
+ */
+#define SMX_GELU_LUT_ENTRIES 4096
+
+/* smx_q4_0_gemv_swiglu with the table GELU in place of SiLU: out[i] =
+ * RNE_bf16(act(g_i) * u_i).  Replaces NativeUp.execute + activate_native
+ * (src/spark_vllm_ascend/kernels/linear.py:540-611). */
+int smx_q4_0_gemv_gelu(void* stream, const void* x, const void* w, const void* lut,
+                       void* out, int64_t d, int64_t k);
+
+/*
  * Q4_0 GEMV whose activation is RMSNorm(x + residual) * gamma, computed by
  * the GEMV itself (norm_ub semantics, as smx_add_rmsnorm):
  *   s = float(x) + float(residual)  (residual may be NULL)
@@ -109,6 +131,15 @@ int smx_q4_0_add_rmsnorm_gemv_swiglu(void* stream, const void* x,
                                      void* residual_out, const void* w,
                                      void* out, int64_t d, int64_t k,
                                      float eps);
+
+/* smx_q4_0_add_rmsnorm_gemv followed by the table GELU of
+ * smx_q4_0_gemv_gelu: the whole of NativeUp.execute (norm_ub, gate/up GEMV,
+ * activate_native; src/spark_vllm_ascend/kernels/linear.py:585-611). */
+int smx_q4_0_add_rmsnorm_gemv_gelu(void* stream, const void* x,
+                                   const void* residual, const void* gamma,
+                                   void* residual_out, const void* w,
+                                   const void* lut, void* out, int64_t d,
+                                   int64_t k, float eps);
 
 /*
  * smx_q4_0_add_rmsnorm_gemv for the LM head (no residual_out) that also
@@ -332,6 +363,15 @@ int smx_silu_mul(void* stream, const void* gate_up, void* out, int64_t rows,
                  int64_t d);
 
 /*
+ * The table GELU of smx_q4_0_gemv_gelu on a [rows, 2*d] bf16 gate|up
+ * tensor: out[r, i] = RNE_bf16(act(g) * u), g = gate_up[r, i], u =
+ * gate_up[r, d + i] (activate_native,
+ * src/spark_vllm_ascend/kernels/linear.py:540-577, on a gate/up product).
+ */
+int smx_gelu_mul(void* stream, const void* gate_up, const void* lut, void* out,
+                 int64_t rows, int64_t d);
+
+/*
  * Embedding row gather: out[t, :] = table[ids[t], :] (bf16); an id outside
  * [0, vocab) writes a zero row.
  * Replaces VocabParallelEmbedding's lookup
@@ -382,6 +422,10 @@ int smx_q4_0_gemm(void* stream, const void* x, const void* w, void* y, int64_t m
  */
 int smx_q4_0_gemm_swiglu(void* stream, const void* x, const void* w, void* out, int64_t m,
                          int64_t d, int64_t k);
+
+/* smx_q4_0_gemm_swiglu with the table GELU of smx_q4_0_gemv_gelu. */
+int smx_q4_0_gemm_gelu(void* stream, const void* x, const void* w, const void* lut, void* out,
+                       int64_t m, int64_t d, int64_t k);
 
 /*
  * smx_q4_0_gemm (x 16-byte aligned) that also writes greedy-argmax keys:

@@ -8,7 +8,8 @@ the decoder residual wiring of src/spark_vllm_ascend/plugin/spark2_5.py:
 287-297,369-376 (the first input norm outside the loop, each layer's output
 normalised by the next layer's input norm, the final norm after the last
 layer).  Shapes and ops are those of the 4B Q4_0 decoder (per-head q/k
-RMSNorm, neox RoPE over the full head, SwiGLU); rounding to bf16 happens at
+RMSNorm, neox RoPE over the full head, SwiGLU -- or the reference model's
+table GELU, cfg activation "gelu"); rounding to bf16 happens at
 every stage output, as in the reference's stage outputs.  GEMVs are float64
 over exactly dequantised weights (q4_0.gemv_f64).
 
@@ -39,7 +40,7 @@ def _gemv(x_f32: np.ndarray, blocks: np.ndarray, n: int, k: int) -> np.ndarray:
 
 class OracleDecoder:
     """cfg: dict with hidden, n_layers, n_q, n_kv, head_dim, intermediate,
-    vocab, eps.  weights: dict of numpy arrays --
+    vocab, eps; optional activation ("swiglu" or "gelu") and gelu_lut.  weights: dict of numpy arrays --
       layers.{i}.qkv / o_proj / gate_up / down : uint8 Q4_0 blocks
       layers.{i}.norm0..3 : float32 values of bf16 (input, post, q, k norms)
       final_norm : float32 values of bf16; head : uint8 Q4_0 blocks
@@ -53,6 +54,11 @@ class OracleDecoder:
         self.cos_sin = cos_sin
         self.num_splits = num_splits
         self.capacity = capacity  # KV capacity the splits are cut from (None: the length)
+        # activation "gelu": the bf16 table of the reference model's GELU
+        # (cfg "gelu_lut", bits; default the correctly rounded table)
+        self.gelu_lut = cfg.get("gelu_lut")
+        if cfg.get("activation") == "gelu" and self.gelu_lut is None:
+            self.gelu_lut = oops.gelu_table()
         c = cfg
         self.embed = bf16_bits_to_f32(oq.dequant_bf16_bits(weights["head"], c["vocab"], c["hidden"]))
         self.reset()
@@ -82,7 +88,10 @@ class OracleDecoder:
         o = _gemv(attn, w[f"layers.{i}.o_proj"], H, nq * hd)
         h2, res = oops.add_rmsnorm(o, res, w[f"layers.{i}.norm1"], eps)
         gu = _gemv(h2, w[f"layers.{i}.gate_up"], 2 * I, H)
-        act = oops.silu_mul(gu[:I], gu[I:])
+        if c.get("activation", "swiglu") == "gelu":  # the reference model's table GELU
+            act = oops.gelu_mul(f32_to_bf16_bits(gu[:I]), gu[I:], self.gelu_lut)
+        else:
+            act = oops.silu_mul(gu[:I], gu[I:])
         d = _gemv(act, w[f"layers.{i}.down"], H, I)
         nxt = w[f"layers.{i + 1}.norm0"] if i + 1 < c["n_layers"] else w["final_norm"]
         return oops.add_rmsnorm(d, res, nxt, eps)

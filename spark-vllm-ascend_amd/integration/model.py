@@ -58,6 +58,10 @@ class DecoderConfig:
     eps: float = 1e-6
     rope_theta: float = 1e6
     block_size: int = 128
+    # gate/up activation: "swiglu" (silu(g) * u) or "gelu", the reference
+    # model's erf-GELU(g) * u through its bf16 table (src/spark_vllm_ascend/
+    # kernels/linear.py:540-577, table at integration/model.py:13-16)
+    activation: str = "swiglu"
 
     @property
     def qkv_rows(self) -> int:
@@ -118,6 +122,8 @@ class DecodeModel:
                  fused: bool = True, batch: int = 1, plan_items: int | None = None):
         if not 1 <= batch <= 16:
             raise ValueError("batch must be in [1, 16]")
+        if cfg.activation not in ("swiglu", "gelu"):
+            raise ValueError(f"activation must be 'swiglu' or 'gelu', got {cfg.activation!r}")
         self.cfg = cfg
         self.batch = B = batch
         self.fused = fused and batch == 1
@@ -160,6 +166,8 @@ class DecodeModel:
                        else synthetic_q4_0(c.vocab, c.hidden, seed * 1000 + 999, self.device))
         self.head = TiedQ4_0Head(head_blocks.to(self.device), c.vocab, c.hidden)
         self.cos_sin = rope_cos_sin_cache(max_len, c.head_dim, c.rope_theta, self.device)
+        # the GELU table the gate/up epilogues read (None: SwiGLU)
+        self.act_lut = torch_ops.gelu_table(self.device) if c.activation == "gelu" else None
         self.scale = 1.0 / math.sqrt(c.head_dim)
         if B == 1:
             self.num_items = 0
@@ -249,7 +257,7 @@ class DecodeModel:
             ops.q4_0_gemv(self.attn, L.o_proj.qweight, c.hidden, c.n_q * c.head_dim, out=self.o)
             ops.add_rmsnorm_gemv_swiglu(self.o, self.res_a, L.post_norm, L.gate_up.qweight,
                                         c.intermediate, c.hidden, c.eps, residual_out=self.res_b,
-                                        out=self.act)
+                                        out=self.act, lut=self.act_lut)
         elif self.batch > 1:
             B = self.batch
             ops.add_rmsnorm(x_in, r_in, L.input_norm, c.eps, out=self.h, residual_out=self.res_a)
@@ -263,7 +271,7 @@ class DecodeModel:
             ops.add_rmsnorm(self.o, self.res_a, L.post_norm, c.eps, out=self.h2,
                             residual_out=self.res_b)
             ops.q4_0_gemm_swiglu(self.h2, L.gate_up.qweight, c.intermediate, c.hidden,
-                                 out=self.act)
+                                 out=self.act, lut=self.act_lut)
             ops.q4_0_gemm(self.act, L.down.qweight, c.hidden, c.intermediate, out=self.d)
             return
         else:
@@ -278,8 +286,12 @@ class DecodeModel:
             ops.q4_0_gemv(self.attn, L.o_proj.qweight, c.hidden, c.n_q * c.head_dim, out=self.o)
             ops.add_rmsnorm(self.o, self.res_a, L.post_norm, c.eps, out=self.h2,
                             residual_out=self.res_b)
-            ops.q4_0_gemv_swiglu(self.h2, L.gate_up.qweight, c.intermediate, c.hidden,
-                                 out=self.act)
+            if self.act_lut is None:
+                ops.q4_0_gemv_swiglu(self.h2, L.gate_up.qweight, c.intermediate, c.hidden,
+                                     out=self.act)
+            else:
+                ops.q4_0_gemv_gelu(self.h2, L.gate_up.qweight, self.act_lut, c.intermediate,
+                                   c.hidden, out=self.act)
         ops.q4_0_gemv(self.act, L.down.qweight, c.hidden, c.intermediate, out=self.d)
 
     def enqueue_step(self) -> None:

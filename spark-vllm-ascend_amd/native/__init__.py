@@ -23,7 +23,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libsmx.so"
 #: spark-vllm-ascend_amd/native/validate.py after a passing GPU test run) to
 #: vouch for the library about to be loaded
 VALIDATION_ENV = "SMX_VALIDATION_RECORD"
-ABI_VERSION = 7
+ABI_VERSION = 8
 SMX_EINVAL = 10001
 SMX_EUNSUPPORTED = 10002
 
@@ -39,6 +39,7 @@ SIGNATURES = {
     "smx_q4_0_dequant_bf16": [_P, _P, _P, _I64, _I64],
     "smx_q4_0_gemv": [_P, _P, _P, _P, _I64, _I64],
     "smx_q4_0_gemv_swiglu": [_P, _P, _P, _P, _I64, _I64],
+    "smx_q4_0_gemv_gelu": [_P, _P, _P, _P, _P, _I64, _I64],
     "smx_splitkv_decode": [_P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32,
                            _I32, _I32, _F32],
     "smx_splitkv_decode_merged": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32,
@@ -57,6 +58,7 @@ SIGNATURES = {
                                                       _I32, _I32, _I32, _I32, _F32, _F32],
     "smx_q4_0_gemm": [_P, _P, _P, _P, _I64, _I64, _I64],
     "smx_q4_0_gemm_swiglu": [_P, _P, _P, _P, _I64, _I64, _I64],
+    "smx_q4_0_gemm_gelu": [_P, _P, _P, _P, _P, _I64, _I64, _I64],
     "smx_q4_0_gemm_argmax": [_P, _P, _P, _P, _P, _I64, _I64, _I64],
     "smx_q4_0_gemm_keys_per_row": [_I64],
     "smx_compute_slot_mapping": [_P, _P, _I32, _P, _P, _P, _I32, _I32, _I32, _I32],
@@ -64,6 +66,7 @@ SIGNATURES = {
     "smx_qknorm_rope_kv_write": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32,
                                  _I32, _I32, _I32, _F32],
     "smx_silu_mul": [_P, _P, _P, _I64, _I64],
+    "smx_gelu_mul": [_P, _P, _P, _P, _I64, _I64],
     "smx_embedding": [_P, _P, _P, _P, _I64, _I64, _I64],
     "smx_argmax_bf16": [_P, _P, _I64, _I64, _P],
     "smx_reshape_and_cache": [_P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32],
@@ -71,6 +74,7 @@ SIGNATURES = {
                            _I32, _P, _P, _I64, _I64],
     "smx_q4_0_add_rmsnorm_gemv": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _F32],
     "smx_q4_0_add_rmsnorm_gemv_swiglu": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _F32],
+    "smx_q4_0_add_rmsnorm_gemv_gelu": [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _F32],
     "smx_q4_0_add_rmsnorm_gemv_argmax": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _F32],
     "smx_q4_0_argmax_keys_size": [_I64, _I64],
     "smx_read_probe_sink_size": [_I64, _I32],

@@ -43,6 +43,7 @@ struct GemmArgs {
   uint16_t* y;        // [m, ldy] bf16
   int m, n_out, npairs;
   int64_t ldx, ldy, up_offset_rows;
+  const uint16_t* act_lut;  // SWIGLU: null for SiLU, else the erf-GELU table (gelu_lut)
 };
 
 __device__ __forceinline__ bf16x8 dequant_word(uint32_t w) {
@@ -143,9 +144,7 @@ __global__ __launch_bounds__(512) void q4_0_gemm_kernel(GemmArgs a) {
       if constexpr (SWIGLU) {
         const int f = blockIdx.x * 8 + nn;
         if (nn < 8 && f < a.n_out) {
-          const float gb = round_bf16(total(nn));
-          const float ub = round_bf16(total(nn + 8));
-          st_agent(a.y + (int64_t)m * a.ldy + f, f32_to_bf16(gb / (1.0f + expf(-gb)) * ub));
+          st_agent(a.y + (int64_t)m * a.ldy + f, gated_act(total(nn), total(nn + 8), a.act_lut));
         }
       } else {
         const int o = blockIdx.x * 16 + nn;
@@ -200,7 +199,7 @@ __device__ __forceinline__ void transpose_rows4(uint32_t& r0, uint32_t& r1, uint
 template <bool SWIGLU, int WS, bool KEYS = false>
 __global__ __launch_bounds__(1024) void q4_0_gemm_tile_kernel(
     const uint8_t* w_, const uint16_t* x_, int npairs, int n_out, int64_t up_offset_rows, int ks,
-    int m, int64_t ldx, uint16_t* y, int64_t ldy, uint64_t* keys) {
+    int m, int64_t ldx, uint16_t* y, int64_t ldy, uint64_t* keys, const uint16_t* act_lut) {
   static_assert(!(SWIGLU && KEYS), "argmax keys are for plain outputs");
   __shared__ f32x4 red[16][64];
   extern __shared__ u32x4 xsl[];  // WS > 0: [ks][8 rows x 32 chunks]
@@ -317,9 +316,7 @@ __global__ __launch_bounds__(1024) void q4_0_gemm_tile_kernel(
       if constexpr (SWIGLU) {
         const int f = blockIdx.x * 8 + nn;
         if (nn < 8 && f < n_out) {
-          const float gb = round_bf16(total(nn));
-          const float ub = round_bf16(total(nn + 8));
-          st_agent(y + (int64_t)mr * ldy + f, f32_to_bf16(gb / (1.0f + expf(-gb)) * ub));
+          st_agent(y + (int64_t)mr * ldy + f, gated_act(total(nn), total(nn + 8), act_lut));
         }
       } else {
         const int o = blockIdx.x * 16 + nn;
@@ -350,7 +347,7 @@ __global__ __launch_bounds__(1024) void q4_0_gemm_tile_kernel(
 template <bool SWIGLU, bool KEYS = false>
 hipError_t launch_gemm_tile(hipStream_t s, const void* x, const void* w, void* y, int64_t m,
                             int64_t n_out, int64_t k, int64_t up_offset_rows,
-                            uint64_t* keys = nullptr) {
+                            uint64_t* keys = nullptr, const uint16_t* act_lut = nullptr) {
   const int npairs = (int)(k / 64);
   const int ntiles = (npairs + 3) / 4;
   const int grid = SWIGLU ? (int)((n_out + 7) / 8) : (int)((n_out + 15) / 16);
@@ -372,7 +369,7 @@ hipError_t launch_gemm_tile(hipStream_t s, const void* x, const void* w, void* y
 #define SMX_GEMM_LAUNCH(W)                                                                      \
   SMX_LAUNCH((q4_0_gemm_tile_kernel<SWIGLU, W, KEYS>), dim3(grid), dim3(64 * ks), lds,  \
                      s, (const uint8_t*)w, (const uint16_t*)x, npairs, (int)n_out,                \
-                     up_offset_rows, ks, (int)m, k, (uint16_t*)y, n_out, keys)
+                     up_offset_rows, ks, (int)m, k, (uint16_t*)y, n_out, keys, act_lut)
   if (ws == 1) SMX_GEMM_LAUNCH(1);
   else if (ws == 2) SMX_GEMM_LAUNCH(2);
   else if (ws == 4) SMX_GEMM_LAUNCH(4);
@@ -406,16 +403,30 @@ extern "C" int smx_q4_0_gemm(void* stream, const void* x, const void* w, void* y
   return (int)hipGetLastError();
 }
 
-extern "C" int smx_q4_0_gemm_swiglu(void* stream, const void* x, const void* w, void* y,
-                                    int64_t m, int64_t d, int64_t k) {
-  SMX_GEMM_CHECKS(d);
+static int gemm_gated(void* stream, const void* x, const void* w, const void* lut, void* y,
+                      int64_t m, int64_t d, int64_t k) {
+  const uint16_t* act_lut = (const uint16_t*)lut;
   if ((uintptr_t)x % 16 == 0)
-    return (int)smx::launch_gemm_tile<true>((hipStream_t)stream, x, w, y, m, d, k, d);
+    return (int)smx::launch_gemm_tile<true>((hipStream_t)stream, x, w, y, m, d, k, d, nullptr,
+                                            act_lut);
   smx::GemmArgs a{(const uint16_t*)x, (const uint8_t*)w, (uint16_t*)y, (int)m, (int)d,
-                  (int)(k / 64), k, d, d};
+                  (int)(k / 64), k, d, d, act_lut};
   SMX_LAUNCH(smx::q4_0_gemm_kernel<true>, dim3((unsigned)((d + 7) / 8)), dim3(512), 0,
                      (hipStream_t)stream, a);
   return (int)hipGetLastError();
+}
+
+extern "C" int smx_q4_0_gemm_swiglu(void* stream, const void* x, const void* w, void* y,
+                                    int64_t m, int64_t d, int64_t k) {
+  SMX_GEMM_CHECKS(d);
+  return gemm_gated(stream, x, w, nullptr, y, m, d, k);
+}
+
+extern "C" int smx_q4_0_gemm_gelu(void* stream, const void* x, const void* w, const void* lut,
+                                  void* y, int64_t m, int64_t d, int64_t k) {
+  SMX_GEMM_CHECKS(d);
+  SMX_REQUIRE(lut && (uintptr_t)lut % 2 == 0, "lut must be non-null and 2-byte aligned");
+  return gemm_gated(stream, x, w, lut, y, m, d, k);
 }
 
 extern "C" int64_t smx_q4_0_gemm_keys_per_row(int64_t n) { return (n + 15) / 16; }

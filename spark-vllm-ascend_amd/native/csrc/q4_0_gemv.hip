@@ -102,6 +102,7 @@ struct GemvArgs {
   const uint8_t* w;
   uint16_t* y;
   uint64_t* argmax_keys;     // EPI_ARGMAX: one key per workgroup
+  const uint16_t* act_lut;   // EPI_SWIGLU: null for SiLU, else the erf-GELU table (gelu_lut)
   int n_out;
   int npairs;
   int64_t up_offset_rows;
@@ -117,6 +118,7 @@ struct GemvTail {
   uint16_t* residual_out;
   uint16_t* y;
   uint64_t* argmax_keys;
+  const uint16_t* act_lut;
   float eps;
 };
 
@@ -130,7 +132,8 @@ struct GemvTail {
 //       and reduce the sum of squares through LDS; workgroup 0 also writes the
 //       new residual), which replaces a separate add+RMSNorm launch.
 //  EPI_SWIGLU: rows 0-3 of a group are gate rows, rows 4-7 the matching up
-//       rows, and the output is silu(gate) * up for 4 features per group.
+//       rows, and the output is act(gate) * up for 4 features per group
+//       (gated_act: SiLU, or erf-GELU through a table).
 //  EPI_ARGMAX: besides y, each workgroup writes the max (value, -index) key
 //       of its rows, for an on-device greedy argmax.
 template <int NPMAX, int RG, bool PRO, int EPI>
@@ -148,6 +151,7 @@ __global__ __launch_bounds__(NPMAX <= 2 ? 1024 : 512) void q4_0_gemv_kernel(
   a.residual_out = tail.residual_out;
   a.y = tail.y;
   a.argmax_keys = tail.argmax_keys;
+  a.act_lut = tail.act_lut;
   a.eps = tail.eps;
   extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
   constexpr bool SWIGLU = EPI == EPI_SWIGLU;
@@ -321,9 +325,7 @@ __global__ __launch_bounds__(NPMAX <= 2 ? 1024 : 512) void q4_0_gemv_kernel(
         if (r < 4 && o < n_out) {
           float up = 0.f;
           for (int i = 0; i < ks; ++i) up += part[i * (8 * RG) + g * 8 + r + 4];
-          const float gb = round_bf16(tot);
-          const float ub = round_bf16(up);
-          st_agent(a.y + o, f32_to_bf16(gb / (1.0f + expf(-gb)) * ub));
+          st_agent(a.y + o, gated_act(tot, up, a.act_lut));
         }
       } else {
         const int o = (blockIdx.x * RG + g) * 8 + r;
@@ -351,7 +353,8 @@ __global__ __launch_bounds__(NPMAX <= 2 ? 1024 : 512) void q4_0_gemv_kernel(
 template <bool SWIGLU>
 __global__ __launch_bounds__(64) void q4_0_gemv_generic_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ w,
-    uint16_t* __restrict__ y, int n_out, int nblocks, int64_t up_offset_rows) {
+    uint16_t* __restrict__ y, int n_out, int nblocks, int64_t up_offset_rows,
+    const uint16_t* act_lut) {
   const int o = blockIdx.x;
   const int lane = threadIdx.x;
   const int64_t row_bytes = (int64_t)nblocks * 18;
@@ -384,9 +387,7 @@ __global__ __launch_bounds__(64) void q4_0_gemv_generic_kernel(
   }
   if (lane == 0) {
     if constexpr (SWIGLU) {
-      const float gb = round_bf16(acc[0]);
-      const float ub = round_bf16(acc[1]);
-      st_agent(y + o, f32_to_bf16(gb / (1.0f + expf(-gb)) * ub));
+      st_agent(y + o, gated_act(acc[0], acc[1], act_lut));
     } else {
       st_agent(y + o, f32_to_bf16(acc[0]));
     }
@@ -426,7 +427,7 @@ static hipError_t launch_fast(hipStream_t s, const GemvArgs& a, int ks) {
   constexpr int OUT_PER_WG = (EPI == EPI_SWIGLU ? 4 : 8) * RG;
   const int grid = (a.n_out + OUT_PER_WG - 1) / OUT_PER_WG;
   const size_t lds = (size_t)ks * NPMAX * 8 * 36 * 4 + (size_t)ks * 8 * RG * 4 + (size_t)ks * 4;
-  const GemvTail tail{a.residual_out, a.y, a.argmax_keys, a.eps};
+  const GemvTail tail{a.residual_out, a.y, a.argmax_keys, a.act_lut, a.eps};
   SMX_LAUNCH((q4_0_gemv_kernel<NPMAX, RG, PRO, EPI>), dim3(grid), dim3(64 * ks), lds, s,
                      a.w, a.x, a.residual, a.gamma, a.npairs, a.n_out, a.up_offset_rows, ks,
                      tail);
@@ -548,10 +549,10 @@ static hipError_t gemv_dispatch(hipStream_t s, GemvArgs a, int64_t k, int epi, b
     if (pro || epi == EPI_ARGMAX) return hipErrorInvalidValue;  // callers check first
     if (epi == EPI_SWIGLU)
       SMX_LAUNCH(q4_0_gemv_generic_kernel<true>, dim3((unsigned)a.n_out), dim3(64), 0, s,
-                         a.x, a.w, a.y, a.n_out, (int)nblocks, a.up_offset_rows);
+                         a.x, a.w, a.y, a.n_out, (int)nblocks, a.up_offset_rows, a.act_lut);
     else
       SMX_LAUNCH(q4_0_gemv_generic_kernel<false>, dim3((unsigned)a.n_out), dim3(64), 0,
-                         s, a.x, a.w, a.y, a.n_out, (int)nblocks, a.up_offset_rows);
+                         s, a.x, a.w, a.y, a.n_out, (int)nblocks, a.up_offset_rows, a.act_lut);
     return hipGetLastError();
   }
   if (pro) {
@@ -602,16 +603,33 @@ extern "C" int smx_q4_0_gemv(void* stream, const void* x, const void* w, void* y
                                  false);
 }
 
-extern "C" int smx_q4_0_gemv_swiglu(void* stream, const void* x, const void* w, void* out,
-                                    int64_t d, int64_t k) {
-  SMX_REQUIRE(x && w && out, "x, w and out must be non-null");
-  SMX_REQUIRE(d >= 1 && d < (1ll << 30), "d out of range");
-  SMX_REQUIRE(k >= 32 && k % 32 == 0 && k <= (1 << 20), "k must be a multiple of 32 in [32, 2^20]");
-  SMX_REQUIRE((uintptr_t)x % 2 == 0 && (uintptr_t)w % 2 == 0 && (uintptr_t)out % 2 == 0,
-              "x, w and out must be 2-byte aligned");
+// Shared checks of the gated (gate/up) GEMV entries.
+#define SMX_GATED_GEMV_CHECKS                                                                    \
+  SMX_REQUIRE(x && w && out, "x, w and out must be non-null");                                   \
+  SMX_REQUIRE(d >= 1 && d < (1ll << 30), "d out of range");                                      \
+  SMX_REQUIRE(k >= 32 && k % 32 == 0 && k <= (1 << 20), "k must be a multiple of 32 in [32, 2^20]"); \
+  SMX_REQUIRE((uintptr_t)x % 2 == 0 && (uintptr_t)w % 2 == 0 && (uintptr_t)out % 2 == 0,         \
+              "x, w and out must be 2-byte aligned")
+
+static int gemv_gated(void* stream, const void* x, const void* w, const void* lut, void* out,
+                      int64_t d, int64_t k) {
   smx::GemvArgs a = plain_args(x, w, out, d);
   a.up_offset_rows = d;
+  a.act_lut = (const uint16_t*)lut;
   return (int)smx::gemv_dispatch((hipStream_t)stream, a, k, smx::EPI_SWIGLU, false);
+}
+
+extern "C" int smx_q4_0_gemv_swiglu(void* stream, const void* x, const void* w, void* out,
+                                    int64_t d, int64_t k) {
+  SMX_GATED_GEMV_CHECKS;
+  return gemv_gated(stream, x, w, nullptr, out, d, k);
+}
+
+extern "C" int smx_q4_0_gemv_gelu(void* stream, const void* x, const void* w, const void* lut,
+                                  void* out, int64_t d, int64_t k) {
+  SMX_GATED_GEMV_CHECKS;
+  SMX_REQUIRE(lut && (uintptr_t)lut % 2 == 0, "lut must be non-null and 2-byte aligned");
+  return gemv_gated(stream, x, w, lut, out, d, k);
 }
 
 // Shared checks of the entries with the add+RMSNorm prologue.
@@ -651,14 +669,30 @@ extern "C" int smx_q4_0_add_rmsnorm_gemv(void* stream, const void* x, const void
       smx::EPI_STORE, true);
 }
 
+static int norm_gemv_gated(void* stream, const void* x, const void* residual, const void* gamma,
+                           void* residual_out, const void* w, const void* lut, void* out,
+                           int64_t d, int64_t k, float eps) {
+  smx::GemvArgs a = norm_args(x, residual, gamma, residual_out, w, out, d, eps);
+  a.up_offset_rows = d;
+  a.act_lut = (const uint16_t*)lut;
+  return (int)smx::gemv_dispatch((hipStream_t)stream, a, k, smx::EPI_SWIGLU, true);
+}
+
 extern "C" int smx_q4_0_add_rmsnorm_gemv_swiglu(void* stream, const void* x, const void* residual,
                                                 const void* gamma, void* residual_out,
                                                 const void* w, void* out, int64_t d, int64_t k,
                                                 float eps) {
   SMX_NORM_GEMV_CHECKS(x, w, out, d);
-  smx::GemvArgs a = norm_args(x, residual, gamma, residual_out, w, out, d, eps);
-  a.up_offset_rows = d;
-  return (int)smx::gemv_dispatch((hipStream_t)stream, a, k, smx::EPI_SWIGLU, true);
+  return norm_gemv_gated(stream, x, residual, gamma, residual_out, w, nullptr, out, d, k, eps);
+}
+
+extern "C" int smx_q4_0_add_rmsnorm_gemv_gelu(void* stream, const void* x, const void* residual,
+                                              const void* gamma, void* residual_out,
+                                              const void* w, const void* lut, void* out,
+                                              int64_t d, int64_t k, float eps) {
+  SMX_NORM_GEMV_CHECKS(x, w, out, d);
+  SMX_REQUIRE(lut && (uintptr_t)lut % 2 == 0, "lut must be non-null and 2-byte aligned");
+  return norm_gemv_gated(stream, x, residual, gamma, residual_out, w, lut, out, d, k, eps);
 }
 
 extern "C" int64_t smx_q4_0_argmax_keys_size(int64_t n, int64_t k) {

@@ -155,6 +155,21 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restric
   stores_done();
 }
 
+// out = bf16(gelu_lut(g) * u): the reference's erf-GELU gate/up activation
+// through its 4096-entry bf16 table.
+__global__ __launch_bounds__(256) void gelu_mul_kernel(const uint16_t* __restrict__ gu,
+                                                       const uint16_t* __restrict__ lut,
+                                                       uint16_t* __restrict__ out, int64_t rows,
+                                                       int64_t d) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // 256 threads per workgroup
+  if (i >= rows * d) return;
+  const int64_t r = i / d, c = i % d;
+  const uint16_t g = gu[r * 2 * d + c];
+  const float u = bf16_bits_to_f32(gu[r * 2 * d + d + c]);
+  st_agent(out + i, f32_to_bf16(bf16_bits_to_f32(gelu_lut(g, lut)) * u));
+  stores_done();
+}
+
 __global__ __launch_bounds__(256) void embedding_kernel(const uint16_t* __restrict__ table,
                                                         const int64_t* __restrict__ ids,
                                                         uint16_t* __restrict__ out, int64_t vocab,
@@ -445,6 +460,19 @@ extern "C" int smx_silu_mul(void* stream, const void* gate_up, void* out, int64_
   SMX_REQUIRE(grid < (1ll << 31), "tensor too large");
   SMX_LAUNCH(smx::silu_mul_kernel, dim3((unsigned)grid), dim3(256), 0,
                      (hipStream_t)stream, (const uint16_t*)gate_up, (uint16_t*)out, rows, d);
+  return (int)hipGetLastError();
+}
+
+extern "C" int smx_gelu_mul(void* stream, const void* gate_up, const void* lut, void* out,
+                            int64_t rows, int64_t d) {
+  SMX_REQUIRE(gate_up && lut && out, "null pointer argument");
+  SMX_REQUIRE((uintptr_t)gate_up % 2 == 0 && (uintptr_t)lut % 2 == 0 && (uintptr_t)out % 2 == 0,
+              "gate_up, lut and out must be 2-byte aligned");
+  SMX_REQUIRE(rows >= 1 && d >= 1 && rows * d < (1ll << 40), "bad shape");
+  const int64_t grid = (rows * d + 255) / 256;
+  SMX_REQUIRE(grid < (1ll << 31), "tensor too large");
+  SMX_LAUNCH(smx::gelu_mul_kernel, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream,
+             (const uint16_t*)gate_up, (const uint16_t*)lut, (uint16_t*)out, rows, d);
   return (int)hipGetLastError();
 }
 

@@ -75,6 +75,33 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t h16) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)h16);
 }
 
+// erf-GELU of a bf16 gate through the table of the reference's gate/up
+// activation (src/spark_vllm_ascend/kernels/linear.py:540-577, table built at
+// src/spark_vllm_ascend/integration/model.py:13-16): lut[0, 2048) holds
+// gelu(g) for the bf16 bit patterns 0x3b00..0x42ff (2^-9 <= g < 128) and
+// lut[2048, 4096) for 0xbb00..0xc2ff (their negatives).  Outside the table:
+// |g| < 2^-9 gives g / 2, g >= 128 gives g (+inf stays +inf), g <= -128
+// gives -0, NaN and -inf give the NaN 0x7fff.
+constexpr int kGeluLutEntries = 4096;
+__device__ __forceinline__ uint16_t gelu_lut(uint32_t g, const uint16_t* lut) {
+  const uint32_t ab = g & 0x7fffu;
+  if (ab > 0x7f80u || g == 0xff80u) return 0x7fffu;
+  if (ab >= 0x4300u) return g < 0x8000u ? (uint16_t)g : (uint16_t)0x8000u;
+  if (ab < 0x3b00u) return f32_to_bf16(0.5f * bf16_bits_to_f32(g));
+  return lut[((ab - 0x3b00u) & 2047u) | ((g >> 4) & 2048u)];
+}
+
+// The gated-MLP activation of the GEMV/GEMM epilogues, on the fp32 sums of a
+// gate row and its up row, each first rounded to bf16 (the GEMV output):
+// silu(g) * u in fp32 when lut is null (SwiGLU), else gelu_lut(g) * u.
+__device__ __forceinline__ uint16_t gated_act(float gate_sum, float up_sum, const uint16_t* lut) {
+  const uint16_t gbits = f32_to_bf16(gate_sum);
+  const float gb = bf16_bits_to_f32(gbits);
+  const float ub = round_bf16(up_sum);
+  if (lut) return f32_to_bf16(bf16_bits_to_f32(gelu_lut(gbits, lut)) * ub);
+  return f32_to_bf16(gb / (1.0f + expf(-gb)) * ub);
+}
+
 // Order-preserving 16-bit key of a bf16 value (NaN above +inf).  Greedy
 // argmax keys are (key << 32) | (0xffffffff - index): the largest key is the
 // largest value, the lowest index among equal values.

@@ -65,16 +65,50 @@ def q4_0_gemv(x: torch.Tensor, w: torch.Tensor, n: int, k: int,
     return out
 
 
-def q4_0_gemv_swiglu(x: torch.Tensor, w: torch.Tensor, d: int, k: int,
-                     out: torch.Tensor | None = None) -> torch.Tensor:
+GELU_LUT_ENTRIES = 4096
+
+
+def gelu_table(device: torch.device | str = "cpu") -> torch.Tensor:
+    """The reference's erf-GELU activation table (src/spark_vllm_ascend/
+    integration/model.py:13-16): gelu(approximate='none') of the bf16 bit
+    patterns 0x3b00..0x42ff, then of 0xbb00..0xc2ff, as 4096 bf16 values.
+    Evaluated by torch on the CPU (the reference evaluates it on its device),
+    then copied to `device`."""
+    bits = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(BF16)
+    full = torch.nn.functional.gelu(bits, approximate="none")
+    return torch.cat((full[0x3B00:0x4300], full[0xBB00:0xC300])).contiguous().to(device)
+
+
+def _lut_checked(lut: torch.Tensor, device: torch.device) -> int:
+    _check(lut, "lut", BF16, GELU_LUT_ENTRIES, device)
+    return lut.data_ptr()
+
+
+def _gemv_gated(x, w, d, k, out, lut):
     _need(k % 32 == 0 and k > 0 and d > 0, "need d > 0 and k a positive multiple of 32")
     _check(x, "x", BF16, k)
     _check(w, "w", torch.uint8, 2 * d * q4_0_row_bytes(k), x.device)
     if out is None:
         out = torch.empty((1, d), dtype=BF16, device=x.device)
     _check(out, "out", BF16, d, x.device)
-    call("smx_q4_0_gemv_swiglu", _stream(x), x.data_ptr(), w.data_ptr(), out.data_ptr(), d, k)
+    if lut is None:
+        call("smx_q4_0_gemv_swiglu", _stream(x), x.data_ptr(), w.data_ptr(), out.data_ptr(), d, k)
+    else:
+        call("smx_q4_0_gemv_gelu", _stream(x), x.data_ptr(), w.data_ptr(),
+             _lut_checked(lut, x.device), out.data_ptr(), d, k)
     return out
+
+
+def q4_0_gemv_swiglu(x: torch.Tensor, w: torch.Tensor, d: int, k: int,
+                     out: torch.Tensor | None = None) -> torch.Tensor:
+    return _gemv_gated(x, w, d, k, out, None)
+
+
+def q4_0_gemv_gelu(x: torch.Tensor, w: torch.Tensor, lut: torch.Tensor, d: int, k: int,
+                   out: torch.Tensor | None = None) -> torch.Tensor:
+    """out [1, d] = act(x W_gate^T) * (x W_up^T), act the table GELU
+    (gelu_table)."""
+    return _gemv_gated(x, w, d, k, out, lut)
 
 
 def splitkv_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
@@ -264,7 +298,7 @@ def qknorm_rope_kv_write(qkv: torch.Tensor, q_gamma: torch.Tensor, k_gamma: torc
     return q_out
 
 
-def silu_mul(gate_up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+def _gated_mul(gate_up, out, lut):
     _check(gate_up, "gate_up", BF16)
     d2 = gate_up.shape[-1]
     _need(d2 % 2 == 0, "last dimension must be even")
@@ -272,8 +306,22 @@ def silu_mul(gate_up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Te
     if out is None:
         out = torch.empty((*gate_up.shape[:-1], d2 // 2), dtype=BF16, device=gate_up.device)
     _check(out, "out", BF16, rows * d2 // 2, gate_up.device)
-    call("smx_silu_mul", _stream(gate_up), gate_up.data_ptr(), out.data_ptr(), rows, d2 // 2)
+    if lut is None:
+        call("smx_silu_mul", _stream(gate_up), gate_up.data_ptr(), out.data_ptr(), rows, d2 // 2)
+    else:
+        call("smx_gelu_mul", _stream(gate_up), gate_up.data_ptr(),
+             _lut_checked(lut, gate_up.device), out.data_ptr(), rows, d2 // 2)
     return out
+
+
+def silu_mul(gate_up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    return _gated_mul(gate_up, out, None)
+
+
+def gelu_mul(gate_up: torch.Tensor, lut: torch.Tensor,
+             out: torch.Tensor | None = None) -> torch.Tensor:
+    """The table GELU (gelu_table) of a [..., 2d] gate|up tensor times up."""
+    return _gated_mul(gate_up, out, lut)
 
 
 def embedding(table: torch.Tensor, ids: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
@@ -402,15 +450,31 @@ def add_rmsnorm_gemv(x: torch.Tensor, residual: torch.Tensor | None, gamma: torc
 def add_rmsnorm_gemv_swiglu(x: torch.Tensor, residual: torch.Tensor | None, gamma: torch.Tensor,
                             w: torch.Tensor, d: int, k: int, eps: float,
                             residual_out: torch.Tensor | None = None,
-                            out: torch.Tensor | None = None) -> torch.Tensor:
+                            out: torch.Tensor | None = None,
+                            lut: torch.Tensor | None = None) -> torch.Tensor:
+    """add+RMSNorm, gate/up GEMV and SwiGLU -- or, given the GELU table
+    (gelu_table) as lut, the reference's table GELU in place of SiLU."""
     _norm_gemv_checks(x, residual, gamma, residual_out, k)
     _check(w, "w", torch.uint8, 2 * d * q4_0_row_bytes(k), x.device)
     if out is None:
         out = torch.empty((1, d), dtype=BF16, device=x.device)
     _check(out, "out", BF16, d, x.device)
-    call("smx_q4_0_add_rmsnorm_gemv_swiglu", _stream(x), x.data_ptr(), _ptr(residual),
-         gamma.data_ptr(), _ptr(residual_out), w.data_ptr(), out.data_ptr(), d, k, float(eps))
+    if lut is None:
+        call("smx_q4_0_add_rmsnorm_gemv_swiglu", _stream(x), x.data_ptr(), _ptr(residual),
+             gamma.data_ptr(), _ptr(residual_out), w.data_ptr(), out.data_ptr(), d, k, float(eps))
+    else:
+        call("smx_q4_0_add_rmsnorm_gemv_gelu", _stream(x), x.data_ptr(), _ptr(residual),
+             gamma.data_ptr(), _ptr(residual_out), w.data_ptr(), _lut_checked(lut, x.device),
+             out.data_ptr(), d, k, float(eps))
     return out
+
+
+def add_rmsnorm_gemv_gelu(x: torch.Tensor, residual: torch.Tensor | None, gamma: torch.Tensor,
+                          w: torch.Tensor, lut: torch.Tensor, d: int, k: int, eps: float,
+                          residual_out: torch.Tensor | None = None,
+                          out: torch.Tensor | None = None) -> torch.Tensor:
+    """NativeUp.execute as one launch: add+RMSNorm, gate/up GEMV, table GELU."""
+    return add_rmsnorm_gemv_swiglu(x, residual, gamma, w, d, k, eps, residual_out, out, lut)
 
 
 def argmax_keys_size(n: int, k: int) -> int:
@@ -552,8 +616,10 @@ def q4_0_gemm(x: torch.Tensor, w: torch.Tensor, n: int, k: int,
 
 
 def q4_0_gemm_swiglu(x: torch.Tensor, w: torch.Tensor, d: int, k: int,
-                     out: torch.Tensor | None = None) -> torch.Tensor:
-    """out [m, d] = silu(x W_gate^T) * (x W_up^T), W = [gate; up] [2d, k]."""
+                     out: torch.Tensor | None = None,
+                     lut: torch.Tensor | None = None) -> torch.Tensor:
+    """out [m, d] = silu(x W_gate^T) * (x W_up^T), W = [gate; up] [2d, k];
+    given the GELU table (gelu_table) as lut, the table GELU in place of SiLU."""
     _need(x.dim() == 2 and x.shape[1] == k and 1 <= x.shape[0] <= 16, "x must be [m <= 16, k]")
     _check(x, "x", BF16)
     _need(x.data_ptr() % 8 == 0, "x must be 8-byte aligned")
@@ -561,9 +627,18 @@ def q4_0_gemm_swiglu(x: torch.Tensor, w: torch.Tensor, d: int, k: int,
     if out is None:
         out = torch.empty((x.shape[0], d), dtype=BF16, device=x.device)
     _check(out, "out", BF16, x.shape[0] * d, x.device)
-    call("smx_q4_0_gemm_swiglu", _stream(x), x.data_ptr(), w.data_ptr(), out.data_ptr(),
-         x.shape[0], d, k)
+    if lut is None:
+        call("smx_q4_0_gemm_swiglu", _stream(x), x.data_ptr(), w.data_ptr(), out.data_ptr(),
+             x.shape[0], d, k)
+    else:
+        call("smx_q4_0_gemm_gelu", _stream(x), x.data_ptr(), w.data_ptr(),
+             _lut_checked(lut, x.device), out.data_ptr(), x.shape[0], d, k)
     return out
+
+
+def q4_0_gemm_gelu(x: torch.Tensor, w: torch.Tensor, lut: torch.Tensor, d: int, k: int,
+                   out: torch.Tensor | None = None) -> torch.Tensor:
+    return q4_0_gemm_swiglu(x, w, d, k, out, lut)
 
 
 def gemm_keys_per_row(n: int) -> int:

@@ -45,6 +45,16 @@ def test_bindings_cover_header():
     ("smx_q4_0_gemv", (None, 16, 16, 16, 0, 256)),
     ("smx_q4_0_gemv", (None, 17, 16, 16, 64, 256)),
     ("smx_q4_0_gemv_swiglu", (None, 16, 16, 16, 64, 100)),
+    ("smx_q4_0_gemv_gelu", (None, 16, 16, None, 16, 64, 256)),
+    ("smx_q4_0_gemv_gelu", (None, 16, 16, 17, 16, 64, 256)),
+    ("smx_q4_0_gemv_gelu", (None, 16, 16, 16, 16, 64, 100)),
+    ("smx_q4_0_add_rmsnorm_gemv_gelu", (None, 16, 32, 16, 64, 16, None, 16, 64, 2560, 1e-6)),
+    ("smx_q4_0_add_rmsnorm_gemv_gelu", (None, 16, 32, 16, 64, 16, 16, 16, 64, 2560, -1.0)),
+    ("smx_q4_0_gemm_gelu", (None, 16, 16, None, 16, 4, 64, 256)),
+    ("smx_q4_0_gemm_gelu", (None, 16, 16, 16, 16, 17, 64, 256)),
+    ("smx_gelu_mul", (None, 16, None, 16, 1, 10)),
+    ("smx_gelu_mul", (None, 16, 16, 16, 0, 10)),
+    ("smx_gelu_mul", (None, 16, 15, 16, 1, 10)),
     ("smx_q4_0_dequant_bf16", (None, 16, 16, 64, 33)),
     ("smx_splitkv_decode", (None, 16, 16, 16, 16, 16, 16, 16, 1, 4, 8, 8, 128, 32, 8, 64, 0.1)),
     ("smx_splitkv_decode", (None, 16, 16, 16, 16, 16, 16, 16, 1, 4, 8, 8, 128, 32, 16, 128, 0.1)),

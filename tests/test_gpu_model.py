@@ -1,7 +1,8 @@
 """GPU parity of the whole decode step against the oracle decoder.
 
   * a 2-layer model (hidden 256): logits within 2e-2 of the float64 oracle
-    at every teacher-forced step, greedy tokens equal except near-ties;
+    at every teacher-forced step, greedy tokens equal except near-ties --
+    with SwiGLU, and with the reference model's table GELU;
   * graph replay equals eager execution bit for bit;
   * one full-size layer (hidden 2560, 32q/8kv, intermediate 9728) at context
     4096 against the oracle layer, within 1e-2;
@@ -51,7 +52,8 @@ def oracle_from(model, num_splits):
     w["final_norm"] = f32_of(model.final_norm)
     w["head"] = model.head.q4_0_head.cpu().numpy()
     cfg = dict(hidden=c.hidden, n_layers=c.n_layers, n_q=c.n_q, n_kv=c.n_kv, head_dim=c.head_dim,
-               intermediate=c.intermediate, vocab=c.vocab, eps=c.eps)
+               intermediate=c.intermediate, vocab=c.vocab, eps=c.eps, activation=c.activation,
+               gelu_lut=None if model.act_lut is None else bits_of(model.act_lut))
     cap = model.state.block_table.shape[1] * c.block_size
     return omodel.OracleDecoder(cfg, w, f32_of(model.cos_sin), num_splits=num_splits, capacity=cap)
 
@@ -94,6 +96,20 @@ def test_tiny_model_teacher_forced(dev, fused):
     seq = rng.integers(0, model.cfg.vocab, 40)
     recs = teacher_forced(model, oracle, seq)
     ties = check_greedy(recs, "tiny")
+    assert ties <= 4
+
+
+@pytest.mark.parametrize("fused", [True, False])
+def test_tiny_model_gelu_teacher_forced(dev, fused):
+    """The reference model's activation (table erf-GELU) in the whole step:
+    same bar as the SwiGLU model; the oracle reads the model's table."""
+    m = _m()
+    cfg = tiny_cfg()
+    cfg.activation = "gelu"
+    model = m.DecodeModel(cfg, dev, seed=4, max_len=64, num_splits=2, fused=fused)
+    oracle = oracle_from(model, num_splits=2)
+    seq = np.random.default_rng(2).integers(0, model.cfg.vocab, 40)
+    ties = check_greedy(teacher_forced(model, oracle, seq), f"tiny gelu fused={fused}")
     assert ties <= 4
 
 
@@ -239,15 +255,19 @@ def test_4b_model_teacher_forced_at_long_context(dev, start):
     check_greedy(recs, f"4B at {start}")
 
 
-@pytest.mark.parametrize("batch", [3, 8, 12])
-def test_batched_decode_against_per_sequence_oracle(dev, batch):
+@pytest.mark.parametrize("batch,activation", [(3, "swiglu"), (8, "swiglu"), (12, "swiglu"),
+                                              (8, "gelu")])
+def test_batched_decode_against_per_sequence_oracle(dev, batch, activation):
     """batch sequences decoded together (MFMA GEMM path: activations staged
     per wave up to 8 rows, read from global memory above), teacher-forced
     with different token streams: every row's logits match that sequence's
-    own oracle decoder at every step."""
+    own oracle decoder at every step (SwiGLU, and the reference model's
+    table GELU in the GEMM epilogue)."""
     import torch
     m = _m()
-    model = m.DecodeModel(tiny_cfg(), dev, seed=8, max_len=64, num_splits=3, batch=batch)
+    cfg = tiny_cfg()
+    cfg.activation = activation
+    model = m.DecodeModel(cfg, dev, seed=8, max_len=64, num_splits=3, batch=batch)
     oracles = [oracle_from(model, num_splits=3) for _ in range(batch)]
     rng = np.random.default_rng(batch)
     T = 12
