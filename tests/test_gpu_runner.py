@@ -3,8 +3,8 @@ include/smx.h): one decode step recorded once and replayed as AQL dispatch
 packets must give eager execution's results bit for bit -- tokens, logits,
 decode state and every KV cache slot -- for the fused and unfused
 one-sequence steps and the batched step, over many steps per replay call and
-over several calls, and the 36-layer 4B-shape model at contexts near 4000
-(one sequence and eight); recording launches nothing; a recording that
+over several calls, with SwiGLU and with the table-GELU activation, and the
+36-layer 4B-shape model at contexts near 4000 (one sequence and eight); recording launches nothing; a recording that
 allocates device memory or raises is refused.  (Eager execution is the reference: a
 graph replays it bit for bit too, but capture() runs a warm-up step that
 writes one KV slot outside the sequences' block tables.)"""
@@ -26,9 +26,9 @@ def _m():
     return pkg("integration.model")
 
 
-def tiny_cfg():
+def tiny_cfg(activation="swiglu"):
     return _m().DecoderConfig(hidden=256, n_layers=2, n_q=8, n_kv=2, head_dim=128,
-                              intermediate=512, vocab=1000, block_size=32)
+                              intermediate=512, vocab=1000, block_size=32, activation=activation)
 
 
 def _state_bits(model):
@@ -48,14 +48,15 @@ def _assert_same(a, b, what):
         np.testing.assert_array_equal(a[k], b[k], err_msg=f"{what}: {k}")
 
 
-def _eager_vs_runner(dev, fences, *, fused=True, batch=1, steps=30, chunks=(30,), seed=5):
+def _eager_vs_runner(dev, fences, *, fused=True, batch=1, steps=30, chunks=(30,), seed=5,
+                     activation="swiglu"):
     import torch
     m = _m()
     kw = dict(seed=seed, max_len=64, num_splits=2, fused=fused)
     if batch > 1:
         kw.update(batch=batch)
-    e = m.DecodeModel(tiny_cfg(), dev, **kw)
-    r = m.DecodeModel(tiny_cfg(), dev, **kw)
+    e = m.DecodeModel(tiny_cfg(activation), dev, **kw)
+    r = m.DecodeModel(tiny_cfg(activation), dev, **kw)
     rng = np.random.default_rng(seed)
     prompts = [torch.tensor(rng.integers(0, 1000, 3 + i)) for i in range(batch)]
     prompt = prompts[0] if batch == 1 else prompts
@@ -90,6 +91,14 @@ def test_runner_replays_the_step(dev, fused, fences):
 @pytest.mark.parametrize("fences", FENCES)
 def test_runner_batched_step(dev, fences):
     _eager_vs_runner(dev, fences, batch=3, chunks=(1, 12, 17))
+
+
+@pytest.mark.parametrize("fused,batch", [(True, 1), (False, 1), (False, 3)])
+def test_runner_replays_the_gelu_model(dev, fused, batch):
+    """The reference model's table-GELU activation (the table pointer is a
+    recorded kernel argument) in the fused, unfused and batched steps."""
+    _eager_vs_runner(dev, "acquire", fused=fused, batch=batch, chunks=(10, 20), seed=8,
+                     activation="gelu")
 
 
 @pytest.mark.parametrize("fences", FENCES)
