@@ -9,6 +9,8 @@ under the namespace ``smx``:
 
   smx::q4_0_gemv(x, w, n, k) -> y                      bf16 [1, n]
   smx::q4_0_gemv_swiglu(x, w, d, k) -> y               bf16 [1, d]
+  smx::q4_0_gemv_gelu(x, w, lut, d, k) -> y            bf16 [1, d] (the
+      reference model's table GELU; lut = torch_ops.gelu_table(device))
   smx::add_rmsnorm(x, residual, gamma, eps) -> (y, residual_out)
   smx::splitkv_decode_attention(q, k_cache, v_cache, block_table, seq_lens,
                                 num_splits, scale) -> out   bf16 [seqs, n_q, hd]
@@ -48,6 +50,15 @@ def register() -> None:
 
     @q4_0_gemv_swiglu.register_fake
     def _(x, w, d, k):
+        return x.new_empty((1, d))
+
+    @torch.library.custom_op(f"{_NS}::q4_0_gemv_gelu", mutates_args=())
+    def q4_0_gemv_gelu(x: torch.Tensor, w: torch.Tensor, lut: torch.Tensor, d: int,
+                       k: int) -> torch.Tensor:
+        return torch_ops.q4_0_gemv_gelu(x.contiguous(), w, lut, d, k)
+
+    @q4_0_gemv_gelu.register_fake
+    def _(x, w, lut, d, k):
         return x.new_empty((1, d))
 
     @torch.library.custom_op(f"{_NS}::add_rmsnorm", mutates_args=())

@@ -64,6 +64,7 @@ class _Entry:
     cos_sin: torch.Tensor
     scale: float
     index: int
+    act_lut: torch.Tensor | None  # the GELU table of a GELU model (None: SwiGLU)
 
 
 def install(model) -> list[str]:
@@ -73,7 +74,8 @@ def install(model) -> list[str]:
     n = len(model.layers)
     for i, L in enumerate(model.layers):
         nxt = model.layers[i + 1].input_norm if i + 1 < n else model.final_norm
-        _layers[L.name] = _Entry(L, nxt, model.cfg, model.cos_sin, model.scale, i)
+        _layers[L.name] = _Entry(L, nxt, model.cfg, model.cos_sin, model.scale, i,
+                                 getattr(model, "act_lut", None))
         names.append(L.name)
     return names
 
@@ -162,7 +164,7 @@ def layer_run(x: torch.Tensor, residual: torch.Tensor, positions: torch.Tensor,
         ops.q4_0_gemv(ws["attn"], L.o_proj.qweight, c.hidden, c.n_q * c.head_dim, out=ws["o"])
         ops.add_rmsnorm_gemv_swiglu(ws["o"], residual, L.post_norm, L.gate_up.qweight,
                                     c.intermediate, c.hidden, c.eps, residual_out=ws["res_a"],
-                                    out=ws["act"])
+                                    out=ws["act"], lut=e.act_lut)
         ops.q4_0_gemv(ws["act"], L.down.qweight, c.hidden, c.intermediate, out=ws["d"])
     else:
         if md.plan is None or md.num_items <= 0:
@@ -177,7 +179,7 @@ def layer_run(x: torch.Tensor, residual: torch.Tensor, positions: torch.Tensor,
         ops.add_rmsnorm(ws["o"], residual, L.post_norm, c.eps, out=ws["h2"],
                         residual_out=ws["res_a"])
         ops.q4_0_gemm_swiglu(ws["h2"], L.gate_up.qweight, c.intermediate, c.hidden,
-                             out=ws["act"])
+                             out=ws["act"], lut=e.act_lut)
         ops.q4_0_gemm(ws["act"], L.down.qweight, c.hidden, c.intermediate, out=ws["d"])
     ops.add_rmsnorm(ws["d"], ws["res_a"], e.next_norm, c.eps, out=y, residual_out=r_out)
     return y, r_out

@@ -130,14 +130,19 @@ def _chain(model, ids, positions, md):
     return y, logits
 
 
-def test_layer_run_one_sequence_matches_step_and_oracle(dev):
+@pytest.mark.parametrize("activation", ["swiglu", "gelu"])
+def test_layer_run_one_sequence_matches_step_and_oracle(dev, activation):
+    """layer_run (the reference's seam) against the decode step and the
+    oracle, with SwiGLU and with the reference model's table GELU."""
     import torch
     m = pkg("integration.model")
     pkg("integration.custom_ops").register()
     lr = pkg("integration.layer_run")
     from test_gpu_model import oracle_from
-    a = m.DecodeModel(_tiny_cfg(), dev, seed=21, max_len=64, num_splits=2)
-    b = m.DecodeModel(_tiny_cfg(), dev, seed=21, max_len=64, num_splits=2)
+    cfg = _tiny_cfg()
+    cfg.activation = activation
+    a = m.DecodeModel(cfg, dev, seed=21, max_len=64, num_splits=2)
+    b = m.DecodeModel(cfg, dev, seed=21, max_len=64, num_splits=2)
     oracle = oracle_from(b, num_splits=2)
     lr.uninstall()
     names = lr.install(b)
@@ -171,17 +176,21 @@ def test_layer_run_one_sequence_matches_step_and_oracle(dev):
     assert ties <= 3
 
 
-def test_layer_run_batched_bitwise_against_batched_step(dev):
+@pytest.mark.parametrize("activation", ["swiglu", "gelu"])
+def test_layer_run_batched_bitwise_against_batched_step(dev, activation):
     """Three sequences: layer_run over the plan computes exactly what the
     decode model's batched step computes (same kernels, same order), so the
-    final normalised hidden state is equal bit for bit at every step."""
+    final normalised hidden state is equal bit for bit at every step (with
+    either activation)."""
     import torch
     m = pkg("integration.model")
     pkg("integration.custom_ops").register()
     lr = pkg("integration.layer_run")
     B, T = 3, 10
-    a = m.DecodeModel(_tiny_cfg(), dev, seed=23, max_len=64, num_splits=3, batch=B)
-    b = m.DecodeModel(_tiny_cfg(), dev, seed=23, max_len=64, num_splits=3, batch=B)
+    cfg = _tiny_cfg()
+    cfg.activation = activation
+    a = m.DecodeModel(cfg, dev, seed=23, max_len=64, num_splits=3, batch=B)
+    b = m.DecodeModel(cfg, dev, seed=23, max_len=64, num_splits=3, batch=B)
     lr.uninstall()
     lr.install(b)
     seqs = np.random.default_rng(23).integers(0, 1000, (B, T))

@@ -45,6 +45,8 @@ def test_fake_shapes():
         w = torch.empty((9728, 1440), dtype=torch.uint8)
         assert torch.ops.smx.q4_0_gemv(x, w, 9728, 2560).shape == (1, 9728)
         assert torch.ops.smx.q4_0_gemv_swiglu(x, w, 4864, 2560).shape == (1, 4864)
+        lut = torch.empty(4096, dtype=torch.bfloat16)
+        assert torch.ops.smx.q4_0_gemv_gelu(x, w, lut, 4864, 2560).shape == (1, 4864)
         y, r = torch.ops.smx.add_rmsnorm(x, x, torch.empty(2560, dtype=torch.bfloat16), 1e-6)
         assert y.shape == r.shape == (1, 2560)
         q = torch.empty((1, 32, 128), dtype=torch.bfloat16)
@@ -75,6 +77,9 @@ def test_custom_ops_match_direct_calls():
                                   bits_of(ops.q4_0_gemv(x, w, 1024, 2560)))
     np.testing.assert_array_equal(bits_of(torch.ops.smx.q4_0_gemv_swiglu(x, w, 512, 2560)),
                                   bits_of(ops.q4_0_gemv_swiglu(x, w, 512, 2560)))
+    lut = ops.gelu_table(dev)
+    np.testing.assert_array_equal(bits_of(torch.ops.smx.q4_0_gemv_gelu(x, w, lut, 512, 2560)),
+                                  bits_of(ops.q4_0_gemv_gelu(x, w, lut, 512, 2560)))
     logits = torch.randn((2, 5000), device=dev).to(torch.bfloat16).float().cpu()
     ids = torch.ops.smx.argmax(logits.to(torch.bfloat16).to(dev)).cpu()
     for r in range(2):  # the first index holding the row maximum
