@@ -7,7 +7,10 @@ splitkv_partials  the reference's split-KV online softmax, AttentionStage
                   tile, m' = max(m, tile max); alpha = exp(m - m'); p =
                   exp(s - m') in fp32; sum = sum * alpha + sum(p); acc = acc *
                   alpha + bf16(p) V; partial = acc / sum, lse = log(sum) + m.
-lse_merge         merge_attention (src/spark_vllm_ascend/kernels/vector.py:
+splitkv_partials_grouped  the same recurrence with all heads advanced
+                  together (batched products), for long-context model runs;
+                  agrees with splitkv_partials to fp32 rounding.
+lse_merge        merge_attention (src/spark_vllm_ascend/kernels/vector.py:
                   45-83) without the output gate: w_s = exp(lse_s - max) /
                   sum, out = bf16(sum_s w_s o_s).
 plan_splits       per-sequence splits from the live lengths (the task list
@@ -96,6 +99,46 @@ def splitkv_partials(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float,
                 m = mn
             po[si, h] = acc / ssum
             pl[si, h] = np.float32(np.log(ssum)) + m
+    return po, pl
+
+
+def splitkv_partials_grouped(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float,
+                             bounds, tile: int = 128):
+    """splitkv_partials with every head advanced together (per tile, one
+    batched fp32 matrix product over the kv heads, each kv head's group of q
+    heads as its columns) instead of one product per q head: the same
+    recurrence and rounding points, for long contexts where the per-head
+    loop is slow.  Products are summed in BLAS order, so results agree with
+    splitkv_partials to fp32 rounding, not bit for bit
+    (tests/test_oracle_attention.py checks the agreement)."""
+    n_q, hd = q.shape
+    n_kv = k.shape[1]
+    g = n_q // n_kv
+    ns = len(bounds)
+    po = np.zeros((ns, n_q, hd), dtype=np.float32)
+    pl = np.full((ns, n_q), -np.inf, dtype=np.float32)
+    qt = q.astype(np.float32).reshape(n_kv, g, hd).transpose(0, 2, 1)  # [n_kv, hd, g]
+    sc = np.float32(scale)
+    for si, (a, b) in enumerate(bounds):
+        if a >= b:
+            continue
+        kk = np.ascontiguousarray(k[a:b].astype(np.float32).transpose(1, 0, 2))  # [n_kv, t, hd]
+        vv = np.ascontiguousarray(v[a:b].astype(np.float32).transpose(1, 0, 2))
+        m = np.full((n_kv, g), -np.inf, dtype=np.float32)
+        ssum = np.zeros((n_kv, g), dtype=np.float32)
+        acc = np.zeros((n_kv, g, hd), dtype=np.float32)
+        for t0 in range(0, b - a, tile):
+            s = (kk[:, t0:t0 + tile] @ qt).astype(np.float32) * sc          # [n_kv, t, g]
+            mn = np.maximum(m, s.max(axis=1)).astype(np.float32)
+            with np.errstate(invalid="ignore"):
+                alpha = np.where(np.isfinite(m), np.exp(m - mn), 0.0).astype(np.float32)
+            p = np.exp((s - mn[:, None, :]).astype(np.float32)).astype(np.float32)
+            ssum = (ssum * alpha + p.sum(axis=1, dtype=np.float32)).astype(np.float32)
+            pv = round_bf16(p).transpose(0, 2, 1) @ vv[:, t0:t0 + tile]     # [n_kv, g, hd]
+            acc = (acc * alpha[:, :, None] + pv).astype(np.float32)
+            m = mn
+        po[si] = (acc / ssum[:, :, None]).reshape(n_q, hd)
+        pl[si] = (np.log(ssum).astype(np.float32) + m).reshape(n_q)
     return po, pl
 
 

@@ -48,25 +48,54 @@ class OracleDecoder:
     """
 
     def __init__(self, cfg: dict, weights: dict, cos_sin: np.ndarray, num_splits: int = 1,
-                 capacity: int | None = None):
+                 capacity: int | None = None, grouped_attention: bool = False):
         self.c = cfg
         self.w = weights
         self.cos_sin = cos_sin
         self.num_splits = num_splits
         self.capacity = capacity  # KV capacity the splits are cut from (None: the length)
+        # long contexts: the grouped split-KV restatement (q heads of a kv
+        # head together; agrees with the per-head one to fp32 rounding)
+        self._partials = (oatt.splitkv_partials_grouped if grouped_attention
+                          else oatt.splitkv_partials)
         # activation "gelu": the bf16 table of the reference model's GELU
         # (cfg "gelu_lut", bits; default the correctly rounded table)
         self.gelu_lut = cfg.get("gelu_lut")
         if cfg.get("activation") == "gelu" and self.gelu_lut is None:
             self.gelu_lut = oops.gelu_table()
         c = cfg
-        self.embed = bf16_bits_to_f32(oq.dequant_bf16_bits(weights["head"], c["vocab"], c["hidden"]))
+        # the tied embedding: bf16 of the dequantised head (the C restatement,
+        # which tests/test_oracle_q4_0.py checks bit for bit against numpy's)
+        self.embed = bf16_bits_to_f32(oq.c_dequant_bf16_bits(weights["head"], c["vocab"],
+                                                             c["hidden"]))
         self.reset()
 
     def reset(self):
         c = self.c
         self.k = [np.zeros((0, c["n_kv"], c["head_dim"]), np.float32) for _ in range(c["n_layers"])]
         self.v = [np.zeros((0, c["n_kv"], c["head_dim"]), np.float32) for _ in range(c["n_layers"])]
+
+    def _append_kv(self, i: int, k: np.ndarray, v: np.ndarray) -> None:
+        """self.k[i] / self.v[i] grow by one token.  They are views of
+        backing arrays with spare rows, so a step copies one token, not the
+        whole cache (a caller may also assign self.k[i] an array of its own:
+        it is moved into a new backing array on the next append)."""
+        if not hasattr(self, "_kv_back"):
+            self._kv_back = {}
+        n = self.k[i].shape[0]
+        back = self._kv_back.get(i)
+        if (back is None or self.k[i].base is not back[0] or self.v[i].base is not back[1]
+                or back[0].shape[0] <= n):
+            cap = max(2 * n, n + 256)
+            kb = np.empty((cap,) + self.k[i].shape[1:], np.float32)
+            vb = np.empty((cap,) + self.v[i].shape[1:], np.float32)
+            kb[:n] = self.k[i]
+            vb[:n] = self.v[i]
+            back = self._kv_back[i] = (kb, vb)
+        back[0][n] = k
+        back[1][n] = v
+        self.k[i] = back[0][:n + 1]
+        self.v[i] = back[1][:n + 1]
 
     def layer(self, i: int, h: np.ndarray, res: np.ndarray, pos: int):
         c, w = self.c, self.w
@@ -79,11 +108,10 @@ class OracleDecoder:
         row = self.cos_sin[pos]
         qr = oops.apply_rope(oops.rms_norm(q, w[f"layers.{i}.norm2"], eps), row)
         kr = oops.apply_rope(oops.rms_norm(k, w[f"layers.{i}.norm3"], eps), row)
-        self.k[i] = np.concatenate((self.k[i], kr[None]), axis=0)
-        self.v[i] = np.concatenate((self.v[i], v[None]), axis=0)
+        self._append_kv(i, kr, v)
         L = pos + 1
-        po, pl = oatt.splitkv_partials(qr, self.k[i][:L], self.v[i][:L], hd ** -0.5,
-                                       oatt.split_bounds(L, self.num_splits, self.capacity))
+        po, pl = self._partials(qr, self.k[i][:L], self.v[i][:L], hd ** -0.5,
+                                oatt.split_bounds(L, self.num_splits, self.capacity))
         attn = oatt.lse_merge(po, pl).reshape(nq * hd)
         o = _gemv(attn, w[f"layers.{i}.o_proj"], H, nq * hd)
         h2, res = oops.add_rmsnorm(o, res, w[f"layers.{i}.norm1"], eps)

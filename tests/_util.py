@@ -48,6 +48,61 @@ def assert_close_rel(got, ref, rtol=1e-2, atol_frac=1e-3, what=""):
             f"got {got.flat[i]!r} ref {ref.flat[i]!r} bound {bound.flat[i]!r}")
 
 
+# unit roundoff of bf16 (8 significant bits): |bf16(x) - x| <= BF16_U |x|
+BF16_U = 2.0 ** -8
+
+
+def assert_attention_close(got, ref, what="", rms_frac=1e-2, l2=1e-2, bf16_out=True):
+    """Attention output at the 1e-2 relative bar against float64 attention:
+    every element within rms_frac of the reference's RMS -- plus, for a bf16
+    output, the output's own rounding (BF16_U |ref|; the reference rounds its
+    output to bf16 too, and that alone reaches 1.4e-2 of the RMS at the
+    largest elements) -- and the relative L2 error below l2.  Returns
+    (max |err| / rms, relative L2)."""
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    rms = float(np.sqrt(np.mean(ref ** 2)))
+    err = np.abs(got - ref)
+    bound = rms_frac * rms + (BF16_U * np.abs(ref) if bf16_out else 0.0)
+    bad = err > bound
+    if bad.any():
+        i = int(np.argmax(err - bound))
+        raise AssertionError(
+            f"{what}: {int(bad.sum())}/{bad.size} beyond {rms_frac} of the rms {rms:.4g}"
+            f"{' + the bf16 rounding' if bf16_out else ''}; worst at {i}: got "
+            f"{got.flat[i]!r} ref {ref.flat[i]!r} (err {err.flat[i] / rms:.4g} rms)")
+    rel = float(np.linalg.norm(got - ref) / max(np.linalg.norm(ref), 1e-300))
+    assert rel <= l2, f"{what}: relative L2 {rel:.4g} > {l2}"
+    return float(err.max() / rms), rel
+
+
+def assert_partials_close(po, pl, opo, opl, what=""):
+    """Split-KV partials against the oracle's restatement of the reference's
+    online softmax (bf16 P): the same empty splits (lse -inf, output 0);
+    every lse within 1e-4; per split, every output element within 2e-2 of
+    that split's RMS and the relative L2 error below 1e-2.  (Both round P to
+    bf16, at running maxima that can differ, so the element bar is twice the
+    merged output's: measured up to 0.99e-2 of the RMS, L2 below 2e-3.)"""
+    po, pl = np.asarray(po, np.float64), np.asarray(pl, np.float64)
+    opo, opl = np.asarray(opo, np.float64), np.asarray(opl, np.float64)
+    fin = np.isfinite(opl)
+    np.testing.assert_array_equal(np.isfinite(pl), fin, err_msg=f"{what}: empty splits")
+    if fin.any():
+        lerr = float(np.max(np.abs(pl[fin] - opl[fin])))
+        assert lerr < 1e-4, f"{what}: lse err {lerr:.3g}"
+    assert np.all(po[~fin] == 0), f"{what}: empty split output not zero"
+    for s in range(po.shape[0]):
+        rows = fin[s]
+        if not rows.any():
+            continue
+        a, b = po[s][rows], opo[s][rows]
+        rms = float(np.sqrt(np.mean(b ** 2)))
+        e = float(np.abs(a - b).max())
+        assert e <= 2e-2 * rms, f"{what}: split {s} err {e / rms:.4g} of the rms"
+        rel = float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-300))
+        assert rel <= 1e-2, f"{what}: split {s} relative L2 {rel:.4g}"
+
+
 def bf16_ulp_diff(a_bits: np.ndarray, b_bits: np.ndarray) -> np.ndarray:
     """Distance in bf16 ulps between two bit arrays (sign-magnitude mapped to
     a monotone integer line; +0 and -0 are 0 apart)."""

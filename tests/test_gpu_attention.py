@@ -1,15 +1,19 @@
 """GPU parity of split-KV decode attention and the LSE merge, through the C
-ABI.  Bars: merged output within 2e-2 absolute of the float64 textbook
-attention (q, K, V ~ N(0,1), outputs are O(0.1)); per-split lse within 1e-3
-and partial outputs within 2e-2 of the oracle's restatement of the
-reference's online softmax."""
+ABI.  Bars (tests/_util.py): the merged bf16 output against the float64
+textbook attention with every element within 1e-2 of the reference's RMS
+plus the output's own bf16 rounding, and relative L2 below 1e-2; per split,
+lse within 1e-4 and the fp32 partial output within 2e-2 of the split's RMS
+(relative L2 below 1e-2) of the oracle's restatement of the reference's
+online softmax (bf16 P).  q, K, V ~ N(0,1): the output's RMS is 0.038 /
+0.026 / 0.021 at contexts 2048 / 4096 / 6144."""
 import numpy as np
 import pytest
 
 from oracle import attention as oatt
 from oracle.bf16 import bf16_bits_to_f32
 
-from _util import bf16_dev, bits_of, f32_of, pkg, randn_bf16
+from _util import (assert_attention_close, assert_partials_close, bf16_dev, bits_of, f32_of, pkg,
+                   randn_bf16)
 
 pytestmark = pytest.mark.gpu
 
@@ -73,16 +77,11 @@ def test_splitkv_vs_fp64(ops, dev, L, splits, merged):
     k = oatt.gather_paged(kf, table[0], L)
     v = oatt.gather_paged(vf, table[0], L)
     ref = oatt.attention_f64(qf[0], k, v, scale)
-    err = np.max(np.abs(out.reshape(N_Q, HD) - ref))
-    assert err < 2e-2, f"merged output err {err}"
+    assert_attention_close(out.reshape(N_Q, HD), ref, f"L={L} splits={splits} merged output")
     # per-split partials against the oracle's online softmax
     bounds = oatt.split_bounds(L, splits, table.shape[1] * bs)
     opo, opl = oatt.splitkv_partials(qf[0], k, v, scale, bounds)
-    finite = np.isfinite(opl)
-    np.testing.assert_array_equal(np.isfinite(pl[0]), finite)
-    assert np.max(np.abs(pl[0][finite] - opl[finite]), initial=0) < 1e-3
-    assert np.max(np.abs(po[0][finite] - opo[finite]), initial=0) < 2e-2
-    assert np.all(po[0][~finite] == 0)
+    assert_partials_close(po[0], pl[0], opo, opl, f"L={L} splits={splits} partials")
 
 
 @pytest.mark.parametrize("bs", [32, 64, 256])
@@ -95,7 +94,7 @@ def test_block_sizes(ops, dev, bs):
     qf, kf, vf = (bf16_bits_to_f32(a) for a in (q, kc, vc))
     ref = oatt.attention_f64(qf[0], oatt.gather_paged(kf, table[0], L),
                              oatt.gather_paged(vf, table[0], L), scale)
-    assert np.max(np.abs(out.reshape(N_Q, HD) - ref)) < 2e-2
+    assert_attention_close(out.reshape(N_Q, HD), ref, f"block size {bs}")
 
 
 @pytest.mark.parametrize("L,bs,splits", [(20000, 32, 1), (9000, 128, 1), (3000, 32, 2)])
@@ -110,7 +109,7 @@ def test_long_wave_chunks(ops, dev, L, bs, splits):
     qf, kf, vf = (bf16_bits_to_f32(a) for a in (q, kc, vc))
     ref = oatt.attention_f64(qf[0], oatt.gather_paged(kf, table[0], L),
                              oatt.gather_paged(vf, table[0], L), scale)
-    assert np.max(np.abs(out.reshape(N_Q, HD) - ref)) < 2e-2
+    assert_attention_close(out.reshape(N_Q, HD), ref, f"L={L} bs={bs} splits={splits}")
 
 
 @pytest.mark.parametrize("merged", [False, True])
@@ -126,7 +125,7 @@ def test_ragged_batch(ops, dev, merged):
     for i, L in enumerate(lengths):
         ref = oatt.attention_f64(qf[i], oatt.gather_paged(kf, table[i], L),
                                  oatt.gather_paged(vf, table[i], L), scale)
-        assert np.max(np.abs(out[i] - ref)) < 2e-2, f"sequence {i} (L={L})"
+        assert_attention_close(out[i], ref, f"sequence {i} (L={L})")
 
 
 def test_page_permutation_invariance(ops, dev):
@@ -154,7 +153,7 @@ def test_equal_keys_give_mean_of_values(ops, dev):
     out, _, _ = _run(ops, dev, q, kc, vc, table, [L], 4, HD ** -0.5)
     vf = oatt.gather_paged(bf16_bits_to_f32(vc), table[0], L)
     ref = np.repeat(vf.mean(axis=0), N_Q // N_KV, axis=0)
-    assert np.max(np.abs(out.reshape(N_Q, HD) - ref)) < 1e-2
+    assert_attention_close(out.reshape(N_Q, HD), ref, "equal keys")
 
 
 def test_merged_equals_two_call_path_bitwise(ops, dev):
@@ -267,11 +266,10 @@ def test_planned_vs_fp64(ops, dev, lengths, bs, items, splits):
             k = oatt.gather_paged(kf, table[i], L)
             v = oatt.gather_paged(vf, table[i], L)
             ref = oatt.attention_f64(qf[i], k, v, scale)
-            assert np.max(np.abs(out[i] - ref)) < 2e-2, f"sequence {i} (L={L})"
+            assert_attention_close(out[i], ref, f"sequence {i} (L={L})")
             opo, opl = oatt.splitkv_partials(qf[i], k, v, scale, sp[i])
             n = len(sp[i])
-            assert np.max(np.abs(pl[i, :n] - opl)) < 1e-3
-            assert np.max(np.abs(po[i, :n] - opo)) < 2e-2
+            assert_partials_close(po[i, :n], pl[i, :n], opo, opl, f"sequence {i} partials")
         n = len(sp[i])
         assert np.all(po[i, n:] == 0) and np.all(pl[i, n:] == -np.inf), f"sequence {i} unused slots"
 
@@ -338,4 +336,4 @@ def test_backend_forward(dev, planned):
         np.testing.assert_array_equal(bits_of(kv[0][blk, off]).reshape(-1), knew[i])
         ref = oatt.attention_f64(qf[i], oatt.gather_paged(kf, table[i], L),
                                  oatt.gather_paged(vf, table[i], L), HD ** -0.5)
-        assert np.max(np.abs(got[i] - ref)) < 2e-2, f"sequence {i}"
+        assert_attention_close(got[i], ref, f"sequence {i}")

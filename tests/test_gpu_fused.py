@@ -7,7 +7,8 @@
     logits the same call wrote (ties -> lowest index, across workgroups);
   * q/k RMSNorm + RoPE + KV write fused into split-KV decode: the cache
     writes equal the standalone q/k-norm kernel's, the attention output
-    matches the two-launch path and the float64 oracle.
+    matches the two-launch path and the float64 oracle (every element within
+    1e-2 of the output's RMS plus its bf16 rounding, relative L2 below 1e-2).
 """
 import numpy as np
 import pytest
@@ -17,7 +18,7 @@ from oracle import ops as oops
 from oracle import q4_0 as oq
 from oracle.bf16 import bf16_bits_to_f32, f32_to_bf16_bits
 
-from _util import (FP32_ACC_SLACK, assert_close_rel, assert_swiglu_bracketed, bf16_dev,
+from _util import (FP32_ACC_SLACK, assert_attention_close, assert_close_rel, assert_swiglu_bracketed, bf16_dev,
                    bf16_ulp_diff, bits_of, f32_of, gemv_abs_sum, pkg, randn_bf16)
 
 pytestmark = pytest.mark.gpu
@@ -214,7 +215,7 @@ def test_fused_qknorm_rope_splitkv(ops, dev, lengths, bs, splits):
         v = oatt.gather_paged(vcn, c["np"]["table"][i], L)
         ref = oatt.attention_f64(qf[i], k, v, HD ** -0.5)
         got = f32_of(out).reshape(ns, N_Q, HD)[i]
-        assert np.abs(got - ref).max() < 2e-2, f"seq {i} (L={L})"
+        assert_attention_close(got, ref, f"seq {i} (L={L})")
 
 
 def test_fused_uses_new_kv_over_stale_slot(ops, dev):
@@ -276,7 +277,7 @@ def test_fused_planned(ops, dev, lengths, bs, items, splits):
         v = oatt.gather_paged(vcn, c["np"]["table"][i], L)
         ref = oatt.attention_f64(qf[i], k, v, HD ** -0.5)
         got = f32_of(out).reshape(ns, N_Q, HD)[i]
-        assert np.abs(got - ref).max() < 2e-2, f"seq {i} (L={L})"
+        assert_attention_close(got, ref, f"seq {i} (L={L})")
 
 
 @pytest.mark.parametrize("given", ["none", "positions_only"])

@@ -9,7 +9,12 @@
   * the 36-layer 4B-shape model: greedy tokens teacher-forced against the
     oracle, disagreements only at near-ties (float64 top-2 margin below 2e-2
     of the top logit), from an empty cache and at contexts 2048-2051 and
-    4093-4096 over a seeded cache (the contexts a decode benchmark times).
+    4093-4096 over a seeded cache, and on the step runner in the decode
+    benchmark's configuration (6272-token block table, 49 splits) at its
+    last positions 6138-6143 and over a 64-token greedy run across a page
+    boundary;
+  * eight 4B sequences at seeded contexts in 512..32768 decoded together
+    (the ragged batch) give each row what the sequence gets decoded alone.
 """
 import numpy as np
 import pytest
@@ -39,7 +44,7 @@ def tiny_cfg(n_layers=2):
                               intermediate=512, vocab=1000, block_size=32)
 
 
-def oracle_from(model, num_splits):
+def oracle_from(model, num_splits, grouped=False):
     c = model.cfg
     w = {}
     for i, L in enumerate(model.layers):
@@ -55,7 +60,8 @@ def oracle_from(model, num_splits):
                intermediate=c.intermediate, vocab=c.vocab, eps=c.eps, activation=c.activation,
                gelu_lut=None if model.act_lut is None else bits_of(model.act_lut))
     cap = model.state.block_table.shape[1] * c.block_size
-    return omodel.OracleDecoder(cfg, w, f32_of(model.cos_sin), num_splits=num_splits, capacity=cap)
+    return omodel.OracleDecoder(cfg, w, f32_of(model.cos_sin), num_splits=num_splits, capacity=cap,
+                                grouped_attention=grouped)
 
 
 def teacher_forced(model, oracle, seq):
@@ -365,3 +371,128 @@ def test_4b_batched_matches_single_sequence(dev):
         if int(np.argmax(bl[r])) != int(np.argmax(sl)):
             top = np.sort(sl)[-2:]
             assert top[1] - top[0] < 2e-2 * abs(top[1]), f"row {r}: greedy tokens differ"
+
+
+def _runner_records(model, oracle, start, seq, forced):
+    """Steps of `model` on its recorded step runner from position `start`
+    (token seq[0] fed first), each run and read back alone; with forced,
+    seq[1:] are fed next, else the model's own greedy tokens.  Each step's
+    fed token also goes to the oracle.  Returns check_greedy records."""
+    import torch
+    st = model.state
+    T = len(seq)
+    model.set_context([start], ids=[int(seq[0])])
+    if forced:
+        st.forced[0, start + 1:start + T] = torch.from_numpy(np.asarray(seq[1:])).to(model.device)
+        st.forced_len.fill_(start + T)
+    recs = []
+    for j in range(T):
+        model.run_steps(1, "acquire")
+        gl = f32_of(model.logits).reshape(-1)
+        gid = int(st.next_ids.item())
+        fed = int(st.tokens[0, start + j].item())
+        assert fed == (int(seq[j]) if forced or j == 0 else recs[-1][0])
+        recs.append((gid, oracle.step(fed, start + j), gl))
+        print(f"4B runner ctx {start + j}: step checked", flush=True)
+    return recs
+
+
+def test_4b_model_at_the_protocol_end_on_the_runner(dev):
+    """The decode benchmark's configuration -- a 6272-token block table (49
+    pages), 49 splits of 128, the step runner with acquire-only fences --
+    at the last positions its protocol decodes (6138-6143), teacher-forced
+    over a seeded cache: every step's logits against the float64 oracle,
+    greedy tokens equal except at near-ties."""
+    m = _m()
+    model = m.DecodeModel(m.DecoderConfig(), dev, seed=4, max_len=6272)
+    assert model.num_splits == 49
+    oracle = oracle_from(model, num_splits=model.num_splits, grouped=True)
+    start, T = 6138, 6
+    fill_kv(model, oracle, start, seed=start)
+    seq = np.random.default_rng(start).integers(0, model.cfg.vocab, T)
+    model.record_runner()
+    try:
+        recs = _runner_records(model, oracle, start, seq, forced=True)
+    finally:
+        model.runner.close()
+    check_greedy(recs, f"4B runner at {start}")
+
+
+def test_4b_greedy_run_across_a_page_boundary_on_the_runner(dev):
+    """64 greedy steps on the step runner (the benchmark's configuration)
+    from position 4064 over a seeded cache, crossing the page boundary at
+    4096: the oracle is fed the model's own tokens, and every step's token
+    equals the oracle's greedy choice except at near-ties, with the logits
+    within the bar throughout (as the reference checks its whole 4096-token
+    run for identical tokens, src/tools/deployment/verify_results.py:31,49)."""
+    m = _m()
+    model = m.DecodeModel(m.DecoderConfig(), dev, seed=6, max_len=6272)
+    oracle = oracle_from(model, num_splits=model.num_splits, grouped=True)
+    start, T = 4064, 64
+    fill_kv(model, oracle, start, seed=start)
+    seq = [int(np.random.default_rng(start).integers(0, model.cfg.vocab))] + [0] * (T - 1)
+    model.record_runner()
+    try:
+        recs = _runner_records(model, oracle, start, seq, forced=False)
+    finally:
+        model.runner.close()
+    ties = check_greedy(recs, f"4B greedy run from {start}")
+    assert ties <= 2
+    pages = {(start + j) // model.cfg.block_size for j in range(T)}
+    assert len(pages) == 2
+
+
+def test_4b_batched_at_ragged_long_contexts_matches_single_sequence(dev):
+    """Eight 4B sequences at seeded contexts drawn from 512..32768 (the
+    ragged-batch workload) over a seeded cache, decoded together for 4
+    teacher-forced steps on the step runner (m = 8 GEMMs, per-sequence split
+    plan): each row's logits at every step match that sequence decoded alone
+    from the same cache contents (GEMVs, capacity splits), within 2e-2 of
+    the logits' scale, with the same greedy token unless the top two are a
+    near-tie.  Same seed, so the same weights."""
+    import torch
+    m = _m()
+    B, T = 8, 4
+    rng = np.random.default_rng(33)
+    ctx = rng.integers(512, 32768 - T, B)
+    seqs = rng.integers(0, m.DecoderConfig().vocab, (B, T))
+    max_len = int(ctx.max()) + T + 1
+    batch = m.DecodeModel(m.DecoderConfig(), dev, seed=7, max_len=max_len, batch=B)
+    batch.fill_kv(int(ctx.sum()))
+    st = batch.state
+    batch.record_runner()
+    blogits = []
+    try:
+        batch.set_context(ctx.tolist(), ids=seqs[:, 0].tolist())
+        for r in range(B):
+            st.forced[r, ctx[r] + 1:ctx[r] + T] = torch.from_numpy(seqs[r, 1:]).to(dev)
+        st.forced_len.copy_(torch.from_numpy(ctx + T).to(torch.int32))
+        for _ in range(T):
+            batch.run_steps(1, "acquire")
+            blogits.append(f32_of(batch.logits).reshape(B, -1))
+    finally:
+        batch.runner.close()
+    print(f"batched 8 x 4 steps at contexts {ctx.tolist()} done", flush=True)
+    single = m.DecodeModel(m.DecoderConfig(), dev, seed=7, max_len=max_len)
+    sst = single.state
+    bs = single.cfg.block_size
+    nb = -(-max_len // bs)
+    for r in range(B):
+        src = st.block_table[r, :nb].long()
+        dst = sst.block_table[0, :nb].long()
+        for Lb, Ls in zip(batch.layers, single.layers):
+            Ls.kv_cache[:, dst] = Lb.kv_cache[:, src]
+        # the batched steps wrote positions ctx..ctx+T-1; the single decode
+        # writes the same values there (compared below through the logits)
+        single.set_context([int(ctx[r])], ids=[int(seqs[r, 0])])
+        sst.forced[0, ctx[r] + 1:ctx[r] + T] = torch.from_numpy(seqs[r, 1:]).to(dev)
+        sst.forced_len.fill_(int(ctx[r]) + T)
+        for j in range(T):
+            single.step()
+            sl = f32_of(single.logits).reshape(-1)
+            assert_close_rel(blogits[j][r], sl, rtol=2e-2, atol_frac=2e-2,
+                             what=f"row {r} (ctx {ctx[r]}) step {j}")
+            if int(np.argmax(blogits[j][r])) != int(np.argmax(sl)):
+                top = np.sort(sl)[-2:]
+                assert top[1] - top[0] < 2e-2 * abs(top[1]), f"row {r} step {j}: tokens differ"
+        print(f"row {r} (ctx {ctx[r]}): 4 steps checked", flush=True)

@@ -146,3 +146,22 @@ def test_planned_partials_merge_to_unsplit(lengths, items, splits):
         ref = oatt.attention_f64(q, k, v, 128 ** -0.5)
         po, pl = oatt.splitkv_partials(q, k, v, 128 ** -0.5, bounds)
         assert np.max(np.abs(oatt.lse_merge(po, pl) - ref)) < 1e-2
+
+
+@pytest.mark.parametrize("L,S", [(1, 4), (33, 3), (300, 2), (1000, 8), (2500, 5)])
+def test_grouped_partials_agree_with_per_head(L, S):
+    """The grouped restatement (q heads of a kv head advanced together, for
+    long contexts) follows the per-head recurrence: same empty splits, lse
+    within a few fp32 ulps, partials within fp32 rounding of each other."""
+    rng = np.random.default_rng(L + 7 * S)
+    q, k, v = rand_case(rng, L)
+    b = oatt.split_bounds(L, S)
+    po, pl = oatt.splitkv_partials(q, k, v, 128 ** -0.5, b)
+    gpo, gpl = oatt.splitkv_partials_grouped(q, k, v, 128 ** -0.5, b)
+    fin = np.isfinite(pl)
+    np.testing.assert_array_equal(np.isfinite(gpl), fin)
+    np.testing.assert_allclose(gpl[fin], pl[fin], rtol=1e-6, atol=1e-6)
+    # a bf16 rounding of p may flip when the scores differ in their last bit
+    np.testing.assert_allclose(gpo, po, rtol=0, atol=4e-3 * np.abs(po).max())
+    assert np.linalg.norm(gpo - po) <= 1e-3 * np.linalg.norm(po)
+    assert np.all(gpo[~fin] == 0)
