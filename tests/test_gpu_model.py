@@ -390,7 +390,9 @@ def _runner_records(model, oracle, start, seq, forced):
         model.run_steps(1, "acquire")
         gl = f32_of(model.logits).reshape(-1)
         gid = int(st.next_ids.item())
-        fed = int(st.tokens[0, start + j].item())
+        # set_context feeds seq[0] as the id itself; each later token was
+        # written at its position by the previous step's advance kernel
+        fed = int(seq[0]) if j == 0 else int(st.tokens[0, start + j].item())
         assert fed == (int(seq[j]) if forced or j == 0 else recs[-1][0])
         recs.append((gid, oracle.step(fed, start + j), gl))
         print(f"4B runner ctx {start + j}: step checked", flush=True)
