@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define SMX_ABI_VERSION 8
+#define SMX_ABI_VERSION 9
 
 /* Return codes besides 0 and hipError_t values. */
 #define SMX_EINVAL 10001      /* an argument failed validation */
@@ -486,23 +486,6 @@ int smx_decode_advance(void* stream, int64_t* next_ids,
                        int64_t hidden);
 
 /*
- * Streaming-read probe (a measurement instrument, no counterpart in the
- * reference): reads `bytes` (a multiple of 16) from src once with 16-byte
- * loads, loads_per_lane (1, 2, 4, 8 or 16) of them per lane all in flight,
- * and writes one uint32 per wave into sink: the XOR of every 32-bit word
- * that wave read.  Workgroups of 4 waves; with L = loads_per_lane, wave w
- * of workgroup b reads the 16-byte words b * 256 * L + i * 256 + 64 * w +
- * lane (i < L, lane < 64), an index past the end reading the last word.
- * Its time is the HBM ceiling of any kernel that moves the same bytes in one
- * launch.
- * sink_size must equal smx_read_probe_sink_size(bytes, loads_per_lane)
- * (-1 for invalid arguments).
- */
-int64_t smx_read_probe_sink_size(int64_t bytes, int32_t loads_per_lane);
-int smx_read_probe(void* stream, const void* src, int64_t bytes, uint32_t* sink,
-                   int64_t sink_size, int32_t loads_per_lane);
-
-/*
  * Step runner: records the kernel launches that the C-ABI calls made on the
  * calling thread between smx_runner_begin and smx_runner_end would enqueue
  * (nothing is launched meanwhile; the calls still validate their arguments
@@ -544,8 +527,17 @@ int smx_runner_wait(smx_runner* runner, double timeout_s);
  * kernel's end (packet-processor timestamps), once it has completed. */
 int smx_runner_elapsed(smx_runner* runner, double* seconds);
 /* Waits (at most 60 s) for running replays, then frees the runner (a runner
- * whose replays do not complete in that time is left allocated). */
+ * whose replays do not complete in that time is left allocated).  A replay
+ * that cannot write all its packets (the queue did not drain within 30 s)
+ * fails and breaks the runner: begin, replay, wait and elapsed then fail
+ * with that reason, and destroy leaves it allocated at once. */
 void smx_runner_destroy(smx_runner* runner);
+
+/* Number of nodes of a HIP graph (a hipGraph_t, e.g. a capture that has
+ * ended): a recording wrapper captures the recorded function on a side
+ * stream and refuses it when any launch besides this library's (which the
+ * recording diverts) reached the stream.  No counterpart in the reference. */
+int smx_graph_num_nodes(void* graph, int64_t* count);
 
 #ifdef __cplusplus
 }

@@ -44,6 +44,7 @@ class SplitKVDecodeMetadata:
     max_seq_len: int = 0          # host hint used only to choose num_splits
     num_items: int = 0            # a plan's split budget (SplitKVDecodeBackend.plan)
     plan: torch.Tensor | None = None  # int32 [num_items + num_seqs, 64] plan records
+    plan_positions: torch.Tensor | None = None  # the positions the plan's records carry
 
 
 def choose_num_splits(capacity: int, tokens_per_split: int = 128, num_seqs: int = 1) -> int:
@@ -164,6 +165,7 @@ class SplitKVDecodeBackend:
             attn_metadata.num_items, po, pl, positions=positions,
             slot_mapping=attn_metadata.slot_mapping if positions is not None else None,
             plan=attn_metadata.plan)
+        attn_metadata.plan_positions = positions
         return attn_metadata
 
     @staticmethod

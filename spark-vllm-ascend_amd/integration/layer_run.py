@@ -39,12 +39,20 @@ Kernel sequence (HIP launches):
           positions and slots): QKV GEMM -> fused planned split-KV + merge
           -> o_proj GEMM -> add + RMSNorm -> gate|up GEMM with SwiGLU -> down
           GEMM -> add + RMSNorm(next norm).
-The reference serves other shapes (prefill) with the stock layer
-(:50-61); this decode path raises for them.
+Other calls -- no published metadata, more than 16 rows, or rows that are
+not one decode token per sequence (prefill) -- go to the stock layer, as the
+reference's op runs vLLM's attention, post-attention norm, MLP and next norm
+for ``x.shape[0] != 1`` or missing metadata (:50-61): install() takes the
+stock layer as a callable ``stock_layer(index, x, residual, positions) ->
+(y, residual_out)`` with the same contract as layer_run.  Without one, such
+calls raise.  With several sequences the positions and KV slots come from
+the step's plan (SplitKVDecodeBackend.plan), so layer_run checks that
+``positions`` is what the plan was built with.
 """
 from __future__ import annotations
 
 from dataclasses import dataclass
+from typing import Callable
 
 import torch
 
@@ -65,17 +73,19 @@ class _Entry:
     scale: float
     index: int
     act_lut: torch.Tensor | None  # the GELU table of a GELU model (None: SwiGLU)
+    stock: Callable | None  # stock_layer(index, x, residual, positions) for other calls
 
 
-def install(model) -> list[str]:
+def install(model, stock_layer: Callable | None = None) -> list[str]:
     """Register every layer of a DecodeModel under its attention layer name
-    with the norm that follows it; returns the names in layer order."""
+    with the norm that follows it, and the stock layer that serves the calls
+    the decode kernels do not (prefill); returns the names in layer order."""
     names = []
     n = len(model.layers)
     for i, L in enumerate(model.layers):
         nxt = model.layers[i + 1].input_norm if i + 1 < n else model.final_norm
         _layers[L.name] = _Entry(L, nxt, model.cfg, model.cos_sin, model.scale, i,
-                                 getattr(model, "act_lut", None))
+                                 getattr(model, "act_lut", None), stock_layer)
         names.append(L.name)
     return names
 
@@ -125,6 +135,26 @@ def _workspace(cfg, rows: int, num_splits: int, device) -> dict:
     return ws
 
 
+def _check_plan_positions(md: SplitKVDecodeMetadata, positions: torch.Tensor) -> None:
+    """Several sequences take their RoPE positions and KV slots from the
+    plan's records, not from `positions`: the two must agree.  The same
+    tensor (what a step passes) passes at once; another tensor is compared
+    by value, which needs a synchronisation, so it is refused under graph
+    capture."""
+    pp = md.plan_positions
+    if md.plan is None or pp is None:
+        raise ValueError("several sequences need this step's split plan built with their "
+                         "positions (SplitKVDecodeBackend.plan(..., positions=...))")
+    if (pp.data_ptr() == positions.data_ptr() and pp.numel() == positions.numel()
+            and pp.dtype == positions.dtype):
+        return
+    if torch.cuda.is_current_stream_capturing():
+        raise ValueError("positions is not the tensor the plan was built with (values cannot "
+                         "be compared during graph capture)")
+    if not torch.equal(pp.to(positions.device).view(-1), positions.view(-1)):
+        raise ValueError("positions differ from those the step's plan was built with")
+
+
 def layer_run(x: torch.Tensor, residual: torch.Tensor, positions: torch.Tensor,
               layer_name: str) -> tuple[torch.Tensor, torch.Tensor]:
     """One decoder layer's decode step; see the module docstring."""
@@ -132,22 +162,30 @@ def layer_run(x: torch.Tensor, residual: torch.Tensor, positions: torch.Tensor,
         raise KeyError(f"layer {layer_name!r} is not installed")
     e = _layers[layer_name]
     md = _metadata
-    if md is None:
-        raise RuntimeError("no attention metadata published: call set_attention_metadata() "
-                           "for this step")
+    T = x.shape[0] if x.dim() == 2 else -1
+    decode = md is not None and 1 <= T <= 16 and md.seq_lens.numel() == T
+    if not decode:
+        if e.stock is not None:  # prefill and unpublished metadata: the stock layer
+            return e.stock(e.index, x, residual, positions)
+        if md is None:
+            raise RuntimeError("no attention metadata published: call set_attention_metadata() "
+                               "for this step (or install a stock layer)")
     c, L = e.cfg, e.layer
     if x.dim() != 2 or x.shape[1] != c.hidden or x.dtype != torch.bfloat16:
         raise ValueError(f"x must be bf16 [T, {c.hidden}], got {x.dtype} {tuple(x.shape)}")
     if tuple(residual.shape) != tuple(x.shape) or residual.dtype != torch.bfloat16:
         raise ValueError("residual must be bf16 of x's shape")
-    T = x.shape[0]
     if positions.numel() != T or positions.dtype != torch.int64:
         raise ValueError("positions must be int64 [T]")
     if md.seq_lens.numel() != T:
         raise ValueError(f"the metadata describes {md.seq_lens.numel()} sequences, x has {T} "
-                         "rows (one decode token per sequence)")
+                         "rows (one decode token per sequence); install a stock layer for "
+                         "prefill")
     if not 1 <= T <= 16:
-        raise ValueError("decode layer_run serves 1..16 sequences; prefill runs the stock layer")
+        raise ValueError("decode layer_run serves 1..16 sequences; install a stock layer for "
+                         "prefill")
+    if T > 1:
+        _check_plan_positions(md, positions)
     x = x.contiguous()
     residual = residual.contiguous()
     ws = _workspace(c, T, md.num_splits, x.device)
@@ -167,7 +205,7 @@ def layer_run(x: torch.Tensor, residual: torch.Tensor, positions: torch.Tensor,
                                     out=ws["act"], lut=e.act_lut)
         ops.q4_0_gemv(ws["act"], L.down.qweight, c.hidden, c.intermediate, out=ws["d"])
     else:
-        if md.plan is None or md.num_items <= 0:
+        if md.num_items <= 0:
             raise ValueError("several sequences need this step's split plan "
                              "(SplitKVDecodeBackend.plan with positions and slots)")
         ops.q4_0_gemm(x, L.qkv.qweight, c.qkv_rows, c.hidden, out=ws["qkv"])

@@ -221,12 +221,18 @@ class DecodeModel:
 
     @classmethod
     def from_gguf(cls, path, device, max_len: int = 8192, num_splits: int | None = None,
-                  block_size: int = 128, fused: bool = True) -> "DecodeModel":
+                  block_size: int = 128, fused: bool = True,
+                  activation: str = "swiglu") -> "DecodeModel":
         """A model whose weights come from a local GGUF file (Q4_0 linears and
-        head, float norms rounded to bf16), shapes from its metadata."""
+        head, float norms rounded to bf16), shapes from its metadata.  GGUF
+        metadata does not name the gate activation, so it is an argument:
+        "swiglu" (the 4B Q4_0 decoder) or "gelu", the reference model's
+        table erf-GELU (src/spark_vllm_ascend/integration/model.py:13-16)."""
         from .gguf_file import GGUFFile, decoder_config, decoder_weights
+        if activation not in ("swiglu", "gelu"):
+            raise ValueError(f"activation must be 'swiglu' or 'gelu', got {activation!r}")
         g = GGUFFile(path)
-        cfg = DecoderConfig(**decoder_config(g), block_size=block_size)
+        cfg = DecoderConfig(**decoder_config(g), block_size=block_size, activation=activation)
         dev = torch.device(device)
         w = {}
         for k, v in decoder_weights(g, cfg.n_layers).items():

@@ -19,11 +19,17 @@ import os
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libsmx.so"
-#: when set, load() requires this validation record (written by
+#: load() requires a validation record (written by
 #: spark-vllm-ascend_amd/native/validate.py after a passing GPU test run) to
-#: vouch for the library about to be loaded
+#: vouch for the library about to be loaded: the one this variable names, or
+#: DEFAULT_RECORD beside the library
 VALIDATION_ENV = "SMX_VALIDATION_RECORD"
-ABI_VERSION = 8
+DEFAULT_RECORD = LIB_PATH.with_name("libsmx.validation.json")
+#: set to 1 to load a library no record vouches for: the test suite, the
+#: benchmark and the build check do (they are what validates and measures the
+#: library as built); a record named by SMX_VALIDATION_RECORD is still checked
+UNVALIDATED_ENV = "SMX_ALLOW_UNVALIDATED"
+ABI_VERSION = 9
 SMX_EINVAL = 10001
 SMX_EUNSUPPORTED = 10002
 
@@ -77,8 +83,6 @@ SIGNATURES = {
     "smx_q4_0_add_rmsnorm_gemv_gelu": [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _F32],
     "smx_q4_0_add_rmsnorm_gemv_argmax": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _F32],
     "smx_q4_0_argmax_keys_size": [_I64, _I64],
-    "smx_read_probe_sink_size": [_I64, _I32],
-    "smx_read_probe": [_P, _P, _I64, _P, _I64, _I32],
     "smx_runner_create": [ctypes.POINTER(ctypes.c_char_p), _I32, ctypes.POINTER(_P)],
     "smx_runner_begin": [_P],
     "smx_runner_end": [_P],
@@ -87,6 +91,7 @@ SIGNATURES = {
     "smx_runner_wait": [_P, _F64],
     "smx_runner_elapsed": [_P, ctypes.POINTER(_F64)],
     "smx_runner_destroy": [_P],
+    "smx_graph_num_nodes": [_P, ctypes.POINTER(_I64)],
 }
 
 #: fence modes of smx_runner_replay (include/smx.h)
@@ -96,10 +101,10 @@ RUNNER_FENCES_ACQUIRE_ONLY = 1
 # return types other than int
 RESTYPES = {"smx_q4_0_argmax_keys_size": ctypes.c_int64,
             "smx_q4_0_gemm_keys_per_row": ctypes.c_int64,
-            "smx_read_probe_sink_size": ctypes.c_int64,
             "smx_runner_destroy": None}
 
 _lib = None
+_record = None  # the validation record load() checked (None: unvalidated load)
 
 
 class SmxError(RuntimeError):
@@ -164,11 +169,32 @@ def check_validation_record(record_path, lib_path: Path = LIB_PATH) -> str:
     return digest
 
 
+def validation_record() -> Path | None:
+    """The validation record load() checks: SMX_VALIDATION_RECORD if set,
+    else DEFAULT_RECORD -- or None when SMX_ALLOW_UNVALIDATED=1 and no
+    record is named."""
+    named = os.environ.get(VALIDATION_ENV)
+    if named:
+        return Path(named)
+    if os.environ.get(UNVALIDATED_ENV, "") == "1":
+        return None
+    return DEFAULT_RECORD
+
+
+def checked_record() -> Path | None:
+    """The record the loaded library was checked against (None: unvalidated)."""
+    return _record
+
+
 def load() -> ctypes.CDLL:
-    """Load libsmx.so once (after torch) and declare its signatures.  With
-    SMX_VALIDATION_RECORD set, the record must vouch for the library first
-    (check_validation_record)."""
-    global _lib
+    """Load libsmx.so once (after torch) and declare its signatures.  A
+    validation record must vouch for the library first
+    (check_validation_record), as the reference refuses its kernel library
+    without one (src/spark_vllm_ascend/integration/head.py:22-27): the record
+    SMX_VALIDATION_RECORD names, else DEFAULT_RECORD; with
+    SMX_ALLOW_UNVALIDATED=1 and no record named, the library loads
+    unchecked."""
+    global _lib, _record
     if _lib is not None:
         return _lib
     try:  # bind to the HIP runtime torch uses when torch is present
@@ -179,8 +205,14 @@ def load() -> ctypes.CDLL:
         raise RuntimeError(
             f"{LIB_PATH} is not built; run __graft_entry__.build() or "
             "python spark-vllm-ascend_amd/native/build.py")
-    record = os.environ.get(VALIDATION_ENV)
-    if record:
+    record = validation_record()
+    if record is not None:
+        if not record.exists():
+            raise RuntimeError(
+                f"no validation record at {record}: validate the library on the GPU first "
+                f"(python spark-vllm-ascend_amd/native/validate.py --record {record}), name a "
+                f"record with {VALIDATION_ENV}, or set {UNVALIDATED_ENV}=1 to load it "
+                "unvalidated")
         check_validation_record(record, LIB_PATH)
     lib = ctypes.CDLL(str(LIB_PATH))
     for name, argtypes in SIGNATURES.items():
@@ -193,6 +225,7 @@ def load() -> ctypes.CDLL:
     if version != ABI_VERSION:
         raise RuntimeError(f"libsmx.so ABI {version} != expected {ABI_VERSION}")
     _lib = lib
+    _record = record
     return lib
 
 

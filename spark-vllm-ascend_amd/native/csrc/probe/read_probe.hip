@@ -4,12 +4,17 @@
 // of what the wave read, so the loads cannot be dropped).  A GEMV or attention
 // launch that moves B bytes cannot beat this kernel on the same B bytes: it
 // has the same launch and first-load latency and no arithmetic.  No
-// counterpart in the reference (a measurement instrument).
-#include "smx_common.h"
-#include "smx_launch.h"
+// counterpart in the reference: a measurement instrument, built into its own
+// library (libsmx_probe.so) that only the benchmark loads, declared in
+// read_probe.h beside this file, never part of libsmx.so.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
 
-namespace smx {
+#include "read_probe.h"
+
 namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 template <int LOADS>
 __global__ __launch_bounds__(256) void read_probe_kernel(const u32x4* __restrict__ src,
@@ -33,9 +38,8 @@ __global__ __launch_bounds__(256) void read_probe_kernel(const u32x4* __restrict
 }
 
 }  // namespace
-}  // namespace smx
 
-#include "smx_abi_util.h"
+extern "C" int32_t smx_probe_abi_version(void) { return SMX_PROBE_ABI_VERSION; }
 
 extern "C" int64_t smx_read_probe_sink_size(int64_t bytes, int32_t loads_per_lane) {
   if (bytes < 16 || bytes % 16 || !(loads_per_lane == 1 || loads_per_lane == 2 ||
@@ -48,24 +52,20 @@ extern "C" int64_t smx_read_probe_sink_size(int64_t bytes, int32_t loads_per_lan
 
 extern "C" int smx_read_probe(void* stream, const void* src, int64_t bytes, uint32_t* sink,
                               int64_t sink_size, int32_t loads_per_lane) {
-  SMX_REQUIRE(src && sink, "src and sink must be non-null");
-  SMX_REQUIRE((uintptr_t)src % 16 == 0 && (uintptr_t)sink % 4 == 0,
-              "src must be 16-byte aligned, sink 4-byte aligned");
+  if (!src || !sink || (uintptr_t)src % 16 != 0 || (uintptr_t)sink % 4 != 0)
+    return SMX_PROBE_EINVAL;
   const int64_t words = smx_read_probe_sink_size(bytes, loads_per_lane);
-  SMX_REQUIRE(words > 0, "bytes must be a positive multiple of 16 and loads_per_lane in "
-                         "{1, 2, 4, 8, 16}");
-  const int64_t grid = words / 4;
-  SMX_REQUIRE(grid < (1ll << 31), "buffer too large");
-  SMX_REQUIRE(sink_size == words, "sink_size must equal smx_read_probe_sink_size(bytes, loads)");
+  if (words <= 0 || words / 4 >= (1ll << 31) || sink_size != words) return SMX_PROBE_EINVAL;
+  const unsigned grid = (unsigned)(words / 4);
   const int64_t n16 = bytes / 16;
   const hipStream_t s = (hipStream_t)stream;
-  const auto* p = reinterpret_cast<const smx::u32x4*>(src);
+  const auto* p = reinterpret_cast<const u32x4*>(src);
   switch (loads_per_lane) {
-    case 1: SMX_LAUNCH(smx::read_probe_kernel<1>, dim3((unsigned)grid), dim3(256), 0, s, p, n16, sink); break;
-    case 2: SMX_LAUNCH(smx::read_probe_kernel<2>, dim3((unsigned)grid), dim3(256), 0, s, p, n16, sink); break;
-    case 4: SMX_LAUNCH(smx::read_probe_kernel<4>, dim3((unsigned)grid), dim3(256), 0, s, p, n16, sink); break;
-    case 8: SMX_LAUNCH(smx::read_probe_kernel<8>, dim3((unsigned)grid), dim3(256), 0, s, p, n16, sink); break;
-    default: SMX_LAUNCH(smx::read_probe_kernel<16>, dim3((unsigned)grid), dim3(256), 0, s, p, n16, sink); break;
+    case 1: hipLaunchKernelGGL(read_probe_kernel<1>, dim3(grid), dim3(256), 0, s, p, n16, sink); break;
+    case 2: hipLaunchKernelGGL(read_probe_kernel<2>, dim3(grid), dim3(256), 0, s, p, n16, sink); break;
+    case 4: hipLaunchKernelGGL(read_probe_kernel<4>, dim3(grid), dim3(256), 0, s, p, n16, sink); break;
+    case 8: hipLaunchKernelGGL(read_probe_kernel<8>, dim3(grid), dim3(256), 0, s, p, n16, sink); break;
+    default: hipLaunchKernelGGL(read_probe_kernel<16>, dim3(grid), dim3(256), 0, s, p, n16, sink); break;
   }
   return (int)hipGetLastError();
 }

@@ -170,6 +170,11 @@ struct smx_runner final : smx::LaunchSink {
   hsa_signal_t first{0};    // completion signal of the first packet (timing)
   uint64_t last_total = 0;  // packets of the last replay
   bool hsa_up = false;
+  // set when a replay could not write all its packets (the queue did not
+  // drain): its last packet, which would bring `pending` back to 0, was never
+  // written, so the runner refuses every later call and is never freed (the
+  // packets already written may still read its kernel arguments)
+  std::string broken;
 
   // recording
   bool recording = false;
@@ -335,8 +340,14 @@ extern "C" int smx_runner_create(const char* const* code_objects, int32_t count,
   return 0;
 }
 
+#define SMX_REQUIRE_WORKING(r)                                                   \
+  do {                                                                           \
+    if (!(r)->broken.empty()) return fail(__func__, "the runner is broken: " + (r)->broken); \
+  } while (0)
+
 extern "C" int smx_runner_begin(smx_runner* r) {
   SMX_REQUIRE(r, "null runner");
+  SMX_REQUIRE_WORKING(r);
   SMX_REQUIRE(!smx::launch_sink(), "this thread is already recording");
   SMX_REQUIRE(hsa_signal_load_scacquire(r->pending) == 0, "a replay is still running");
   r->release_kernargs();
@@ -379,7 +390,9 @@ extern "C" int smx_runner_num_packets(const smx_runner* r, int64_t* out) {
 }
 
 extern "C" int smx_runner_replay(smx_runner* r, int32_t repeats, int32_t fences) {
-  SMX_REQUIRE(r && r->ready, "nothing recorded");
+  SMX_REQUIRE(r, "null runner");
+  SMX_REQUIRE_WORKING(r);
+  SMX_REQUIRE(r->ready, "nothing recorded");
   SMX_REQUIRE(repeats >= 1 && repeats <= 1000000, "repeats must be in [1, 1e6]");
   SMX_REQUIRE(fences == SMX_RUNNER_FENCES_AGENT || fences == SMX_RUNNER_FENCES_ACQUIRE_ONLY,
               "unknown fence mode");
@@ -394,19 +407,27 @@ extern "C" int smx_runner_replay(smx_runner* r, int32_t repeats, int32_t fences)
   r->last_total = total;
   uint64_t idx = 0;
   for (uint64_t i = 0; i < total; ++i) {
-    idx = hsa_queue_add_write_index_relaxed(q, 1);
-    // wait (bounded) for the slot: the packet processor frees it when it has
-    // consumed the packet written q->size packets earlier
-    if (idx - hsa_queue_load_read_index_scacquire(q) >= q->size) {
-      hsa_signal_store_screlease(q->doorbell_signal, (hsa_signal_value_t)(idx - 1));
+    // wait (bounded) for a free slot before claiming it: the packet processor
+    // frees a slot when it has consumed the packet written q->size packets
+    // earlier.  The queue has one producer (this runner, one call at a time),
+    // so the index seen here is the one the claim below returns.
+    const uint64_t next = hsa_queue_load_write_index_relaxed(q);
+    if (next - hsa_queue_load_read_index_scacquire(q) >= q->size) {
+      if (i > 0)  // let the packet processor see this replay's packets so far
+        hsa_signal_store_screlease(q->doorbell_signal, (hsa_signal_value_t)(next - 1));
       const double t0 = now_s();
-      while (idx - hsa_queue_load_read_index_scacquire(q) >= q->size) {
+      while (next - hsa_queue_load_read_index_scacquire(q) >= q->size) {
         if (now_s() - t0 > 30.0) {
-          // the packets already written still run; the queue cannot take this one
-          return fail(__func__, "the queue did not drain within 30 s");
+          // nothing claimed; the packets already written still run, but the
+          // replay's last packet (the one that signals `pending`) is never
+          // written, so the runner cannot be waited on or reused
+          r->broken = "a replay stopped after " + std::to_string(i) + " of " +
+                      std::to_string(total) + " packets: the queue did not drain within 30 s";
+          return fail(__func__, r->broken);
         }
       }
     }
+    idx = hsa_queue_add_write_index_relaxed(q, 1);
     const Packet& p = r->packets[i % r->packets.size()];
     hsa_kernel_dispatch_packet_t* d = base + (idx & mask);
     d->workgroup_size_x = p.block[0];
@@ -442,6 +463,7 @@ extern "C" int smx_runner_replay(smx_runner* r, int32_t repeats, int32_t fences)
 
 extern "C" int smx_runner_wait(smx_runner* r, double timeout_s) {
   SMX_REQUIRE(r, "null runner");
+  SMX_REQUIRE_WORKING(r);
   SMX_REQUIRE(timeout_s > 0.0, "timeout must be positive");
   const double t0 = now_s();
   while (hsa_signal_wait_scacquire(r->pending, HSA_SIGNAL_CONDITION_EQ, 0, 1000000,
@@ -453,6 +475,7 @@ extern "C" int smx_runner_wait(smx_runner* r, double timeout_s) {
 
 extern "C" int smx_runner_elapsed(smx_runner* r, double* seconds) {
   SMX_REQUIRE(r && seconds, "null argument");
+  SMX_REQUIRE_WORKING(r);
   SMX_REQUIRE(r->last_total > 0, "nothing replayed");
   SMX_REQUIRE(hsa_signal_load_scacquire(r->pending) == 0, "a replay is still running");
   hsa_amd_profiling_dispatch_time_t t_first{}, t_last{};
@@ -476,10 +499,24 @@ extern "C" void smx_runner_destroy(smx_runner* r) {
   if (!r) return;
   if (smx::launch_sink() == r) smx::launch_sink() = nullptr;
   // never free memory a running replay reads: wait for it (bounded) first,
-  // and leak the runner if it does not drain
+  // and leak the runner if it does not drain -- or if a replay broke it, as
+  // its `pending` count never returns to 0
+  if (!r->broken.empty()) {
+    fprintf(stderr, "smx step runner: %s; the runner is not freed\n", r->broken.c_str());
+    return;
+  }
   if (hsa_signal_load_scacquire(r->pending) != 0 && smx_runner_wait(r, 60.0) != 0) {
     fprintf(stderr, "smx step runner: a replay still runs after 60 s; the runner is not freed\n");
     return;
   }
   delete r;
+}
+
+extern "C" int smx_graph_num_nodes(void* graph, int64_t* count) {
+  SMX_REQUIRE(graph && count, "null argument");
+  size_t n = 0;
+  const hipError_t e = hipGraphGetNodes(static_cast<hipGraph_t>(graph), nullptr, &n);
+  if (e != hipSuccess) return (int)e;
+  *count = (int64_t)n;
+  return 0;
 }

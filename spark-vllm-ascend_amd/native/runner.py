@@ -18,19 +18,22 @@ as long as the runner replays them; ``record`` refuses a function that
 allocated device memory while it recorded (a temporary freed afterwards
 would leave a dangling pointer in the packets; the allocation count it
 checks is the process's, so another thread allocating meanwhile also makes
-it refuse).  Only this library's calls
-are recorded: a torch operation inside the recorded function would run at
-recording time instead.
+it refuse).  Only this library's calls are recorded, so ``record`` also
+refuses a function that launched anything else -- a torch ``copy_`` or
+``fill_`` into a preallocated buffer, another library's kernel -- which no
+replay would repeat: the function runs under a HIP graph capture on a side
+stream (this thread only), where such a launch becomes a graph node instead
+of running, and a capture with any node is refused.
 """
 from __future__ import annotations
 
 import ctypes
-import os
+import warnings
 
 import torch
 
-from . import (RUNNER_FENCES_ACQUIRE_ONLY, RUNNER_FENCES_AGENT, VALIDATION_ENV, SmxError, call,
-               check_code_objects, load)
+from . import (RUNNER_FENCES_ACQUIRE_ONLY, RUNNER_FENCES_AGENT, SmxError, call,
+               check_code_objects, checked_record, load)
 from .build import code_object_paths
 
 FENCES = {"agent": RUNNER_FENCES_AGENT, "acquire": RUNNER_FENCES_ACQUIRE_ONLY}
@@ -51,8 +54,8 @@ class StepRunner:
         if missing:
             raise RuntimeError(f"device code objects not built: {missing}; run "
                                "__graft_entry__.build()")
-        record = os.environ.get(VALIDATION_ENV)
-        if record:  # the record that vouched for the library vouches for these
+        record = checked_record()
+        if record is not None:  # the record that vouched for the library vouches for these
             check_code_objects(record, paths)
         arr = (ctypes.c_char_p * len(paths))(*[str(p).encode() for p in paths])
         handle = ctypes.c_void_p()
@@ -64,24 +67,44 @@ class StepRunner:
     # ------------------------------------------------------------- recording
     def record(self, fn) -> int:
         """Record the launches fn() makes through this library; returns the
-        number of packets.  Nothing runs on the GPU meanwhile."""
+        number of packets.  Nothing runs on the GPU meanwhile: fn runs under
+        a graph capture of this thread's launches on a side stream, and a
+        function that launched anything outside the library is refused."""
         if self._h is None:
             raise RuntimeError("the runner is closed")
         self._ready = False
         torch.cuda.synchronize()
-        before = _allocations()
-        call("smx_runner_begin", self._h)
-        try:
-            fn()
-        except BaseException:
-            self._lib.smx_runner_end(self._h)  # stop recording; the error wins
-            raise
-        after = _allocations()
-        call("smx_runner_end", self._h)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        graph = torch.cuda.CUDAGraph(keep_graph=True)  # kept for counting, never instantiated
+        with warnings.catch_warnings():
+            # an empty capture is the expected outcome
+            warnings.filterwarnings("ignore", message=".*Graph is empty.*")
+            with torch.cuda.graph(graph, stream=side, capture_error_mode="thread_local"):
+                before = _allocations()
+                call("smx_runner_begin", self._h)
+                try:
+                    fn()
+                except BaseException:
+                    self._lib.smx_runner_end(self._h)  # stop recording; the error wins
+                    raise
+                after = _allocations()
+                ended = self._lib.smx_runner_end(self._h)
+                end_error = self._lib.smx_last_error().decode() if ended else ""
+        nodes = ctypes.c_int64(-1)
+        call("smx_graph_num_nodes", ctypes.c_void_p(graph.raw_cuda_graph()), ctypes.byref(nodes))
+        del graph
+        if ended != 0:
+            raise SmxError("smx_runner_end", ended, end_error)
         if after != before:
             raise RuntimeError(
                 f"the recorded function allocated device memory {after - before} time(s); "
                 "pass preallocated outputs so no recorded pointer can dangle")
+        if nodes.value != 0:
+            raise RuntimeError(
+                f"the recorded function launched {nodes.value} operation(s) outside this "
+                "library (a torch op, another library's kernel): no replay would repeat "
+                "them; only smx_* calls can be recorded")
         self._ready = True
         return self.num_packets
 

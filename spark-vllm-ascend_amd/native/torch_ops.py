@@ -663,22 +663,3 @@ def q4_0_gemm_argmax(x: torch.Tensor, w: torch.Tensor, n: int, k: int, keys: tor
     call("smx_q4_0_gemm_argmax", _stream(x), x.data_ptr(), w.data_ptr(), out.data_ptr(),
          keys.data_ptr(), m, n, k)
     return out
-
-
-def read_probe_sink_size(nbytes: int, loads_per_lane: int) -> int:
-    """Workgroups (sink words) of read_probe over nbytes."""
-    from . import load
-    return int(load().smx_read_probe_sink_size(nbytes, loads_per_lane))
-
-
-def read_probe(src: torch.Tensor, nbytes: int, sink: torch.Tensor, loads_per_lane: int = 8) -> None:
-    """Streaming read of the first nbytes of src (a measurement instrument:
-    the HBM ceiling of a kernel moving the same bytes); sink int32 receives
-    one XOR word per workgroup."""
-    _need(src.is_cuda and src.is_contiguous(), "src must be a contiguous device tensor")
-    _need(0 < nbytes <= src.numel() * src.element_size(), "nbytes exceeds src")
-    _need(src.data_ptr() % 16 == 0 and nbytes % 16 == 0, "src and nbytes must be 16-byte aligned")
-    n = read_probe_sink_size(nbytes, loads_per_lane)
-    _need(n > 0, "loads_per_lane must be 1, 2, 4, 8 or 16")
-    _check(sink, "sink", torch.int32, n, src.device)
-    call("smx_read_probe", _stream(src), src.data_ptr(), nbytes, sink.data_ptr(), n, loads_per_lane)

@@ -1,8 +1,13 @@
-"""pytest configuration: the `gpu` marker and package import."""
+"""pytest configuration: the `gpu` marker and package import.  The suite
+loads the library as built (it is the run that validates it), so it sets
+SMX_ALLOW_UNVALIDATED before anything loads libsmx.so."""
+import os
 import sys
 from pathlib import Path
 
 import pytest
+
+os.environ.setdefault("SMX_ALLOW_UNVALIDATED", "1")
 
 ROOT = Path(__file__).resolve().parent.parent
 if str(ROOT) not in sys.path:

@@ -140,8 +140,18 @@ def test_argmax_keys_follow_launch_shape():
 
 
 def test_read_probe_sizes():
-    lib = pkg("native").load()
+    """The benchmark's streaming-read probe lives in libsmx_probe.so, not in
+    the decode path's library or header."""
+    lib = pkg("native.probe").load()
     assert lib.smx_read_probe_sink_size(14_008_320, 8) == 4 * -(-14_008_320 // 32768)
     assert lib.smx_read_probe_sink_size(100, 8) == -1   # not a multiple of 16
     assert lib.smx_read_probe_sink_size(4096, 3) == -1  # loads not a power of two <= 16
-    assert lib.smx_read_probe(None, 16, 4096, 16, 2, 1) == pkg("native").SMX_EINVAL  # sink size
+    assert lib.smx_read_probe(None, 16, 4096, 16, 2, 1) == 10001  # sink size
+    assert not hasattr(pkg("native").load(), "smx_read_probe")
+    assert "read_probe" not in (ROOT / "include" / "smx.h").read_text()
+
+
+def test_graph_num_nodes_rejects_null():
+    native = pkg("native")
+    n = ctypes.c_int64(-1)
+    assert native.load().smx_graph_num_nodes(None, ctypes.byref(n)) == native.SMX_EINVAL

@@ -165,9 +165,11 @@ def test_decoder_mapping(tmp_path):
 
 
 @pytest.mark.gpu
-def test_model_from_gguf_against_oracle(tmp_path):
+@pytest.mark.parametrize("activation", ["swiglu", "gelu"])
+def test_model_from_gguf_against_oracle(tmp_path, activation):
     """A decoder loaded from a GGUF file, teacher-forced against the oracle
-    decoder built from the same file's tensors."""
+    decoder built from the same file's tensors -- with SwiGLU, and with the
+    reference model's table GELU named at load time."""
     import torch
     from oracle import model as omodel
     from oracle.bf16 import round_bf16
@@ -175,13 +177,20 @@ def test_model_from_gguf_against_oracle(tmp_path):
     p, _ = tiny_qwen3_file(tmp_path)
     mm = pkg("integration.model")
     dev = torch.device("cuda:0")
-    model = mm.DecodeModel.from_gguf(p, dev, max_len=64, num_splits=2, block_size=32)
+    model = mm.DecodeModel.from_gguf(p, dev, max_len=64, num_splits=2, block_size=32,
+                                     activation=activation)
+    assert model.cfg.activation == activation and (model.act_lut is not None) == (
+        activation == "gelu")
     g = gf().GGUFFile(p)
     cfg = gf().decoder_config(g)
     w = {k: (round_bf16(v) if v.dtype == np.float32 else v)
          for k, v in gf().decoder_weights(g, cfg["n_layers"]).items()}
     ocfg = {k: cfg[k] for k in ("hidden", "n_layers", "n_q", "n_kv", "head_dim", "intermediate",
                                 "vocab", "eps")}
+    ocfg["activation"] = activation
+    if activation == "gelu":
+        from _util import bits_of
+        ocfg["gelu_lut"] = bits_of(model.act_lut)
     cap = model.state.block_table.shape[1] * 32
     oracle = omodel.OracleDecoder(ocfg, w, f32_of(model.cos_sin), num_splits=2, capacity=cap)
     seq = np.array([3, 17, 200, 5, 77, 128, 9, 250])
@@ -192,3 +201,9 @@ def test_model_from_gguf_against_oracle(tmp_path):
         ol = oracle.step(int(tok), pos)
         assert_close_rel(f32_of(model.logits).reshape(-1), ol, rtol=2e-2, atol_frac=2e-2,
                          what=f"logits at {pos}")
+
+
+def test_from_gguf_rejects_an_unknown_activation(tmp_path):
+    mm = pkg("integration.model")
+    with pytest.raises(ValueError, match="activation"):
+        mm.DecodeModel.from_gguf(tmp_path / "unused.gguf", "cpu", activation="relu")

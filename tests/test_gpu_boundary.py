@@ -347,3 +347,70 @@ def test_layer_run_rejects_what_it_cannot_serve(dev):
                          torch.zeros(2, dtype=torch.int64, device=dev), name)
     finally:
         lr.uninstall()
+
+
+def test_layer_run_defers_to_the_stock_layer(dev):
+    """As the reference's op runs the stock layer for x.shape[0] != 1 or
+    missing metadata (src/spark_vllm_ascend/integration/model.py:50-61), the
+    seam hands prefill-shaped calls and calls without published metadata to
+    the installed stock layer, with its arguments unchanged; decode calls
+    never reach it."""
+    import torch
+    m = pkg("integration.model")
+    lr = pkg("integration.layer_run")
+    model = m.DecodeModel(_tiny_cfg(), dev, seed=1, max_len=64, num_splits=2)
+    calls = []
+
+    def stock(index, x, residual, positions):
+        calls.append((index, tuple(x.shape), positions.tolist()))
+        return x + 1, residual
+
+    lr.uninstall()
+    names = lr.install(model, stock_layer=stock)
+    try:
+        h = torch.zeros((1, 256), dtype=torch.bfloat16, device=dev)
+        p = torch.zeros(1, dtype=torch.int64, device=dev)
+        y, r = lr.layer_run(h, h, p, names[1])  # no metadata published
+        assert calls == [(1, (1, 256), [0])] and float(y.float().min()) == 1.0
+        md, p1 = _metadata(model, [4])
+        lr.set_attention_metadata(md)
+        x20 = torch.zeros((20, 256), dtype=torch.bfloat16, device=dev)
+        p20 = torch.arange(20, device=dev)
+        lr.layer_run(x20, x20, p20, names[0])  # more rows than the decode kernels serve
+        x3 = torch.zeros((3, 256), dtype=torch.bfloat16, device=dev)
+        lr.layer_run(x3, x3, p20[:3], names[0])  # three tokens of one sequence: prefill
+        assert [c[:2] for c in calls[1:]] == [(0, (20, 256)), (0, (3, 256))]
+        lr.layer_run(torch.randn((1, 256), device=dev).to(torch.bfloat16), h, p1, names[0])
+        torch.cuda.synchronize()
+        assert len(calls) == 3  # the decode token ran the HIP kernels
+    finally:
+        lr.uninstall()
+
+
+def test_layer_run_checks_positions_against_the_plan(dev):
+    """Several sequences take positions and slots from the step's plan:
+    layer_run accepts the plan's own positions tensor or an equal one, and
+    refuses positions that differ from the plan's."""
+    import torch
+    m = pkg("integration.model")
+    lr = pkg("integration.layer_run")
+    B = 3
+    model = m.DecodeModel(_tiny_cfg(), dev, seed=2, max_len=64, num_splits=3, batch=B)
+    lr.uninstall()
+    names = lr.install(model)
+    try:
+        md, pos = _metadata(model, [5, 9, 2], num_items=model.num_items, plan=True)
+        lr.set_attention_metadata(md)
+        x = torch.randn((B, 256), device=dev).to(torch.bfloat16)
+        y1, _ = lr.layer_run(x, x, pos, names[0])
+        y2, _ = lr.layer_run(x, x, pos.clone(), names[0])
+        torch.cuda.synchronize()
+        assert y1.shape == y2.shape == (B, 256)
+        with pytest.raises(ValueError, match="differ"):
+            lr.layer_run(x, x, pos + 1, names[0])
+        md_np, _ = _metadata(model, [5, 9, 2], num_items=model.num_items, plan=False)
+        lr.set_attention_metadata(md_np)
+        with pytest.raises(ValueError, match="plan"):
+            lr.layer_run(x, x, pos, names[0])
+    finally:
+        lr.uninstall()

@@ -1,4 +1,5 @@
-"""The streaming-read probe the benchmark measures HBM ceilings with reads
+"""The streaming-read probe the benchmark measures HBM ceilings with
+(libsmx_probe.so, a library of its own beside the decode path's) reads
 every byte it is given: each wave's sink word equals the XOR of the 32-bit
 words it read (wave w of workgroup b: 16-byte words b*256*L + i*256 + 64*w +
 lane, i < L; the last workgroup's clamped loads re-read the final 16 bytes,
@@ -26,7 +27,7 @@ def _host_xor(words: np.ndarray, loads: int, nwords: int) -> np.ndarray:
 @pytest.mark.parametrize("loads", [1, 2, 4, 8, 16])
 def test_read_probe_xor(nbytes, loads):
     import torch
-    ops = pkg("native.torch_ops")
+    ops = pkg("native.probe")
     dev = torch.device("cuda:0")
     rng = np.random.default_rng(nbytes + loads)
     words = rng.integers(0, 2 ** 32, nbytes // 4, dtype=np.uint32)

@@ -4,8 +4,9 @@ packets must give eager execution's results bit for bit -- tokens, logits,
 decode state and every KV cache slot -- for the fused and unfused
 one-sequence steps and the batched step, over many steps per replay call and
 over several calls, with SwiGLU and with the table-GELU activation, and the
-36-layer 4B-shape model at contexts near 4000 (one sequence and eight); recording launches nothing; a recording that
-allocates device memory or raises is refused.  (Eager execution is the reference: a
+36-layer 4B-shape model at contexts near 4000 (one sequence and eight);
+recording launches nothing; a recording that allocates device memory,
+launches anything outside the library or raises is refused.  (Eager execution is the reference: a
 graph replays it bit for bit too, but capture() runs a warm-up step that
 writes one KV slot outside the sequences' block tables.)"""
 import numpy as np
@@ -136,6 +137,17 @@ def test_recording_refuses_allocations_and_errors(dev):
         with pytest.raises(native.SmxError, match="multiple of 32"):
             runner.record(lambda: native.call("smx_q4_0_gemv", None, 16, 16, 16, 64, 100))
         y = torch.empty(1, 64, dtype=torch.bfloat16, device=dev)
+        # a launch outside the library (here torch's fill_ into a preallocated
+        # buffer) would run once and vanish from every replay: refused, and
+        # it did not run while recording either
+        y.fill_(2.0)
+        torch.cuda.synchronize()
+        with pytest.raises(RuntimeError, match="outside this library"):
+            runner.record(lambda: (ops.q4_0_gemv(x, w, 64, 256, out=y), y.fill_(5.0)))
+        torch.cuda.synchronize()
+        assert float(y.float().min()) == 2.0 and float(y.float().max()) == 2.0
+        with pytest.raises(RuntimeError, match="nothing recorded"):
+            runner.replay(1)
         assert runner.record(lambda: ops.q4_0_gemv(x, w, 64, 256, out=y)) == 1
         y.fill_(1.0)
         runner.run(3)

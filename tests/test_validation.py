@@ -1,9 +1,11 @@
 """The validation-gated load of libsmx.so (CPU): native.load() refuses the
-library unless the record named by SMX_VALIDATION_RECORD vouches for it --
-complete, this ABI version, a GPU test run without failures, the library's
-sha256 -- as the reference refuses its kernel library without a complete
-validation record whose digest matches (src/spark_vllm_ascend/integration/
-head.py:22-27)."""
+library unless a record vouches for it -- the one SMX_VALIDATION_RECORD
+names, else the default record beside the library; complete, this ABI
+version, a GPU test run without failures, the library's sha256 -- as the
+reference refuses its kernel library without a complete validation record
+whose digest matches (src/spark_vllm_ascend/integration/head.py:22-27).
+Only SMX_ALLOW_UNVALIDATED=1 (what this suite, the benchmark and the build
+check set) loads an unvalidated library."""
 import json
 import os
 import subprocess
@@ -114,3 +116,32 @@ def test_default_record_lists_the_built_code_objects(tmp_path):
     rec = pkg("native.validate").make_record(
         0, {"passed": 1, "failed": 0, "errors": 0, "skipped": 0}, native.LIB_PATH)
     assert set(rec["code_objects_sha256"]) == {p.name for p in build.code_object_paths()}
+
+
+def _load_in_fresh_process(env):
+    code = ("import __graft_entry__ as g; g.load_package(); "
+            "import spark_vllm_ascend_amd.native as n; n.load(); print('loaded', n.checked_record())")
+    return subprocess.run([sys.executable, "-c", code], cwd=ROOT, env=env, capture_output=True,
+                          text=True, timeout=300)
+
+
+def test_load_requires_a_record_by_default():
+    """No variable set and no record beside the library: load() refuses and
+    says how to validate; SMX_ALLOW_UNVALIDATED=1 loads it unchecked."""
+    native = pkg("native")
+    if native.DEFAULT_RECORD.exists():
+        pytest.skip("a validation record sits beside the library on this machine")
+    env = {k: v for k, v in os.environ.items()
+           if k not in ("SMX_VALIDATION_RECORD", "SMX_ALLOW_UNVALIDATED")}
+    res = _load_in_fresh_process(env)
+    assert res.returncode != 0 and "no validation record" in res.stderr, res.stderr[-2000:]
+    assert "validate.py" in res.stderr
+    res = _load_in_fresh_process(dict(env, SMX_ALLOW_UNVALIDATED="1"))
+    assert res.returncode == 0 and "loaded None" in res.stdout, res.stderr[-2000:]
+
+
+def test_a_named_record_is_checked_even_when_unvalidated_loads_are_allowed(tmp_path):
+    path = _record(tmp_path, library_sha256="e" * 64)
+    env = dict(os.environ, SMX_VALIDATION_RECORD=str(path), SMX_ALLOW_UNVALIDATED="1")
+    res = _load_in_fresh_process(env)
+    assert res.returncode != 0 and "rejected" in res.stderr
