@@ -227,20 +227,34 @@ def attention_roofline(dev, reps: int, ctxs=ATTN_CTXS, splits_list=ATTN_SPLITS):
 COPY_BYTES = 64 << 20
 
 
-def counter_workload(dev):
-    """Eager launches for a hardware-counter run (rocprofv3 --pmc): a plain
-    device copy of COPY_BYTES (the calibration kernel: it reads and writes
-    exactly COPY_BYTES), then the 9728x2560 GEMV over 24 rotating weight
-    sets, then split-KV decode + merge at context 6144 over 12 KV sets, then
-    the streaming-read probe over the GEMV's weight sets."""
+def counter_workload(dev, steps: int = 2):
+    """Eager launches for a hardware-counter run (rocprofv3 --pmc), each part
+    at the configuration it is reported for:
+      * a plain device copy of COPY_BYTES, five times (the calibration
+        kernel: it reads and writes exactly COPY_BYTES);
+      * the 9728x2560 GEMV over 24 weight sets, twice, then the
+        streaming-read probe over the same sets (the roofline kernel);
+      * split-KV decode + LSE merge at context 6144 with the decode step's
+        49 capacity splits (a 49-page block table), over 12 KV sets;
+      * `steps` decode steps of the 36-layer 4B model at the benchmark's
+        configuration (49-page block table, 49 splits, seeded KV cache,
+        context 4096): every kernel of the step, 36 times per step;
+      * `steps` steps of the 8-sequence batch at seeded contexts in
+        512..32768 (MFMA GEMMs at m = 8, per-sequence split plan).
+    rocprofv3 reads counters per dispatch with cold caches, so no part
+    rotates buffers for cache reasons; the parts are told apart by kernel
+    name and grid size."""
     import torch
+    from spark_vllm_ascend_amd.integration.model import DecodeModel, DecoderConfig
     from spark_vllm_ascend_amd.integration.weights import synthetic_q4_0
+    from spark_vllm_ascend_amd.native import probe
     from spark_vllm_ascend_amd.native import torch_ops as ops
     src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
     dst = torch.empty_like(src)
     for _ in range(5):
         dst.copy_(src)
     torch.cuda.synchronize()
+    del src, dst
     ws = [synthetic_q4_0(GEMV_N, GEMV_K, 500 + i, dev) for i in range(24)]
     x = torch.randn(GEMV_K, device=dev).to(torch.bfloat16)
     y = torch.empty((1, GEMV_N), dtype=torch.bfloat16, device=dev)
@@ -248,14 +262,14 @@ def counter_workload(dev):
         for w in ws:
             ops.q4_0_gemv(x, w, GEMV_N, GEMV_K, out=y)
     torch.cuda.synchronize()
-    from spark_vllm_ascend_amd.native import probe
     sink = torch.empty(probe.read_probe_sink_size(GEMV_W_BYTES, 8), dtype=torch.int32, device=dev)
     for w in ws:
         probe.read_probe(w.view(-1), GEMV_W_BYTES, sink, 8)
     torch.cuda.synchronize()
     del ws
     n_q, n_kv, hd, bs = 32, 8, 128, 128
-    nblk = 6144 // bs
+    nblk = CAPACITY // bs  # 49 pages: the step's table and split count
+    S = nblk
     caches = [(torch.randn((nblk, bs, n_kv, hd), device=dev).to(torch.bfloat16),
                torch.randn((nblk, bs, n_kv, hd), device=dev).to(torch.bfloat16))
               for _ in range(12)]
@@ -263,14 +277,37 @@ def counter_workload(dev):
     table = table.view(1, -1).to(dev)
     q = torch.randn((1, n_q, hd), device=dev).to(torch.bfloat16)
     seq_lens = torch.tensor([6144], dtype=torch.int32, device=dev)
-    S = 48
     po = torch.empty((1, S, n_q, hd), dtype=torch.float32, device=dev)
     pl = torch.empty((1, S, n_q), dtype=torch.float32, device=dev)
     for kc, vc in caches:
         ops.splitkv_decode_merged(q, kc, vc, table, seq_lens, S, hd ** -0.5, po, pl)
     torch.cuda.synchronize()
+    del caches
+    # the decode step at the benchmark's configuration
+    model = DecodeModel(DecoderConfig(), dev, seed=0, max_len=CAPACITY)
+    model.fill_kv(1234)
+    model.set_context([4095], ids=[1])
+    for _ in range(steps):
+        model.step()
+    torch.cuda.synchronize()
+    step_splits = model.num_splits
+    del model
+    torch.cuda.empty_cache()
+    # the 8-sequence batch
+    ctx = torch.randint(512, 32768, (8,), generator=torch.Generator().manual_seed(5))
+    bm = DecodeModel(DecoderConfig(), dev, seed=5, max_len=int(ctx.max()) + steps + 2, batch=8)
+    bm.fill_kv(5)
+    bm.set_context(ctx.tolist())
+    for _ in range(steps):
+        bm.step()
+    torch.cuda.synchronize()
+    plan = (bm.num_items, bm.num_splits)
+    del bm
+    torch.cuda.empty_cache()
     return {"copy_bytes": COPY_BYTES, "gemv_bytes": GEMV_BYTES, "gemv_launches": 48,
-            "read_probe_launches": 24, "attn_launches": 12, "attn_splits": S}
+            "read_probe_launches": 24, "attn_launches": 12, "attn_splits": S,
+            "step": {"context": 4096, "steps": steps, "num_splits": step_splits},
+            "batch": {"contexts": ctx.tolist(), "steps": steps, "plan": plan}}
 
 
 def build_model(dev, max_len: int, num_splits: int | None, seed: int = 0):

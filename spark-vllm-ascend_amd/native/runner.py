@@ -23,7 +23,10 @@ refuses a function that launched anything else -- a torch ``copy_`` or
 ``fill_`` into a preallocated buffer, another library's kernel -- which no
 replay would repeat: the function runs under a HIP graph capture on a side
 stream (this thread only), where such a launch becomes a graph node instead
-of running, and a capture with any node is refused.
+of running, and a capture with any node is refused.  Other threads may
+launch meanwhile (on their own streams) but must not synchronise the whole
+device while a recording runs: HIP refuses a device-wide synchronisation
+while any stream is capturing.
 """
 from __future__ import annotations
 

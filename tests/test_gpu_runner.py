@@ -214,7 +214,10 @@ def test_runner_4b_model_matches_eager(dev, batch):
 
 def test_recording_is_per_thread(dev):
     """While one thread records, a library call on another thread launches
-    as usual (the recording runner is the calling thread's)."""
+    as usual (the recording runner is the calling thread's).  The other
+    thread launches on a stream of its own and does not synchronise the
+    device meanwhile: HIP refuses a device-wide synchronisation while the
+    recording's capture runs."""
     import threading
     import torch
     native = pkg("native")
@@ -224,12 +227,14 @@ def test_recording_is_per_thread(dev):
     w = torch.zeros(64, 8 * 18, dtype=torch.uint8, device=dev)
     y_rec = torch.full((1, 64), 1.0, dtype=torch.bfloat16, device=dev)
     y_other = torch.full((1, 64), 1.0, dtype=torch.bfloat16, device=dev)
+    torch.cuda.synchronize()
     inside, done = threading.Event(), threading.Event()
+    other_stream = torch.cuda.Stream(device=dev)
 
     def other():
         inside.wait(30)
-        ops.q4_0_gemv(x, w, 64, 256, out=y_other)  # launched now, on this thread's stream
-        torch.cuda.synchronize()
+        with torch.cuda.stream(other_stream):
+            ops.q4_0_gemv(x, w, 64, 256, out=y_other)  # launched now, on this thread's stream
         done.set()
 
     t = threading.Thread(target=other)
