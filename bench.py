@@ -811,8 +811,9 @@ def main() -> int:
         graph_cmp["runner_gpu_ms_per_step"] = round(statistics.median(gpu_runs) * 1e3, 4)
     if executor == "runner":  # the same steps once through the captured graph
         g_tpot, g_toks, _ = one_run("graph")
-        graph_cmp = {"graph_ms_per_step": round(g_tpot * 1e3, 4),
-                     "tokens_equal_graph_vs_runner": bool(torch.equal(g_toks, token_runs[0]))}
+        graph_cmp.update({"graph_ms_per_step": round(g_tpot * 1e3, 4),
+                          "tokens_equal_graph_vs_runner": bool(torch.equal(g_toks,
+                                                                           token_runs[0]))})
         log(f"graph: TPOT {g_tpot * 1e3:.4f} ms")
         model.runner.close()
     gen = token_runs[0][args.prompt_len:] if protocol else token_runs[0]
