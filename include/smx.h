@@ -528,10 +528,15 @@ int smx_runner_wait(smx_runner* runner, double timeout_s);
 int smx_runner_elapsed(smx_runner* runner, double* seconds);
 /* Waits (at most 60 s) for running replays, then frees the runner (a runner
  * whose replays do not complete in that time is left allocated).  A replay
- * that cannot write all its packets (the queue did not drain within 30 s)
- * fails and breaks the runner: begin, replay, wait and elapsed then fail
- * with that reason, and destroy leaves it allocated at once. */
+ * that cannot write all its packets (no queue slot freed within the drain
+ * timeout, 30 s unless set below) fails and breaks the runner: begin,
+ * replay, wait and elapsed then fail with that reason, and destroy leaves it
+ * allocated at once (the packets already written still run and read its
+ * kernel arguments). */
 void smx_runner_destroy(smx_runner* runner);
+/* How long a replay waits for a free queue slot before it breaks the runner
+ * (0..3600 s; a failure-handling test sets 0). */
+int smx_runner_set_drain_timeout(smx_runner* runner, double seconds);
 
 /* Number of nodes of a HIP graph (a hipGraph_t, e.g. a capture that has
  * ended): a recording wrapper captures the recorded function on a side

@@ -91,6 +91,7 @@ SIGNATURES = {
     "smx_runner_wait": [_P, _F64],
     "smx_runner_elapsed": [_P, ctypes.POINTER(_F64)],
     "smx_runner_destroy": [_P],
+    "smx_runner_set_drain_timeout": [_P, _F64],
     "smx_graph_num_nodes": [_P, ctypes.POINTER(_I64)],
 }
 

@@ -175,6 +175,7 @@ struct smx_runner final : smx::LaunchSink {
   // written, so the runner refuses every later call and is never freed (the
   // packets already written may still read its kernel arguments)
   std::string broken;
+  double drain_timeout_s = 30.0;  // how long a replay waits for a free queue slot
 
   // recording
   bool recording = false;
@@ -417,12 +418,12 @@ extern "C" int smx_runner_replay(smx_runner* r, int32_t repeats, int32_t fences)
         hsa_signal_store_screlease(q->doorbell_signal, (hsa_signal_value_t)(next - 1));
       const double t0 = now_s();
       while (next - hsa_queue_load_read_index_scacquire(q) >= q->size) {
-        if (now_s() - t0 > 30.0) {
+        if (now_s() - t0 > r->drain_timeout_s) {
           // nothing claimed; the packets already written still run, but the
           // replay's last packet (the one that signals `pending`) is never
           // written, so the runner cannot be waited on or reused
           r->broken = "a replay stopped after " + std::to_string(i) + " of " +
-                      std::to_string(total) + " packets: the queue did not drain within 30 s";
+                      std::to_string(total) + " packets: the queue did not drain in time";
           return fail(__func__, r->broken);
         }
       }
@@ -458,6 +459,13 @@ extern "C" int smx_runner_replay(smx_runner* r, int32_t repeats, int32_t fences)
     if ((i & 255) == 255) hsa_signal_store_screlease(q->doorbell_signal, (hsa_signal_value_t)idx);
   }
   hsa_signal_store_screlease(q->doorbell_signal, (hsa_signal_value_t)idx);
+  return 0;
+}
+
+extern "C" int smx_runner_set_drain_timeout(smx_runner* r, double seconds) {
+  SMX_REQUIRE(r, "null runner");
+  SMX_REQUIRE(seconds >= 0.0 && seconds <= 3600.0, "seconds must be in [0, 3600]");
+  r->drain_timeout_s = seconds;
   return 0;
 }
 

@@ -130,6 +130,11 @@ class StepRunner:
             torch.cuda.synchronize()
         call("smx_runner_replay", self._h, int(repeats), FENCES[fences])
 
+    def set_drain_timeout(self, seconds: float) -> None:
+        """How long a replay waits for a free queue slot before it gives up
+        and breaks the runner (default 30 s)."""
+        call("smx_runner_set_drain_timeout", self._h, float(seconds))
+
     def wait(self, timeout_s: float = 60.0) -> None:
         """Block until every replay has completed (SmxError after timeout_s)."""
         call("smx_runner_wait", self._h, float(timeout_s))

@@ -155,6 +155,42 @@ def test_recording_refuses_allocations_and_errors(dev):
         runner.wait(1.0)  # idle: returns at once
 
 
+# models whose buffers a broken runner's already-written packets may still read: kept alive
+# for the rest of the process
+_KEEP = []
+
+
+def test_a_replay_that_cannot_drain_breaks_the_runner(dev):
+    """Forced from the host: with a zero drain timeout, a replay of far more packets than the
+    runner's queue holds (16384) gives up at the first full queue while the GPU works through
+    the packets already written (they all run to the end: the model's block table covers
+    every position they reach).  The runner then refuses replay, wait, elapsed and a new
+    recording with the reason, and closing it leaves it allocated instead of waiting on a
+    completion signal that the unwritten last packet would have sent."""
+    import time
+    import torch
+    SmxError = pkg("native").SmxError
+    m = _m()
+    model = m.DecodeModel(tiny_cfg(), dev, seed=4, max_len=4096, num_splits=2)
+    model.reset(torch.tensor([5, 6, 7]))
+    runner = model.record_runner()
+    _KEEP.append((model, runner))
+    runner.set_drain_timeout(0.0)
+    reps = 3000  # 3000 steps x 14 packets; positions stay below max_len even if all ran
+    assert runner.num_packets * reps > 2 * 16384
+    with pytest.raises(SmxError, match="did not drain"):
+        runner.replay(reps, "acquire")
+    for fn in (lambda: runner.wait(1.0), runner.elapsed, lambda: runner.replay(1, "acquire")):
+        with pytest.raises(SmxError, match="broken"):
+            fn()
+    with pytest.raises(SmxError, match="broken"):
+        runner.record(model.enqueue_step)
+    time.sleep(0.5)  # the written packets finish meanwhile (tiny kernels, a few ms)
+    runner.close()   # left allocated, with a message; returns at once
+    with pytest.raises(pkg("native").SmxError):
+        pkg("native").call("smx_runner_set_drain_timeout", None, 1.0)
+
+
 def test_runner_elapsed_is_gpu_time_of_the_last_replay(dev):
     import time
     import torch
