@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define SMX_ABI_VERSION 9
+#define SMX_ABI_VERSION 10
 
 /* Return codes besides 0 and hipError_t values. */
 #define SMX_EINVAL 10001      /* an argument failed validation */
@@ -439,6 +439,45 @@ int smx_q4_0_gemm_gelu(void* stream, const void* x, const void* w, const void* l
 int64_t smx_q4_0_gemm_keys_per_row(int64_t n);
 int smx_q4_0_gemm_argmax(void* stream, const void* x, const void* w, void* y, uint64_t* keys,
                          int64_t m, int64_t n, int64_t k);
+
+/*
+ * Packed Q4_0 layout for the GEMMs above: the same codes and fp16 scales as
+ * the GGUF blocks (lossless), moved so that each lane of a wave loads its
+ * MFMA operands directly.  Per row group (16 rows; gated: 8 gate rows then
+ * the 8 matching up rows) and 256-k chunk, 2304 bytes: lane l's 16 bytes for
+ * blocks 0-3 at 16 l, for blocks 4-7 at 1024 + 16 l (word i = block i, byte
+ * b = codes of elements 8 (l >> 4) + b and + 4 + b, low and high nibble), then
+ * row (l & 15)'s 8 fp16 scales at 2048 + 16 (l & 15).  Groups past the last
+ * row repeat it.  The reference repacks its Q4_0 weights into its own
+ * kernel's tile layout at load time (pack, src/spark_vllm_ascend/
+ * integration/weights.py:42-54, cached per layer by packed(), integration/
+ * model.py:8-23, with bf16-exact scales asserted); this is the MFMA
+ * counterpart, keeping the fp16 scales.
+ *
+ * smx_q4_0_packed_bytes: bytes of the packed form of an [n, k] matrix
+ * (gated != 0: the [2d, k] gate|up matrix of the SwiGLU/GELU GEMM, n = d),
+ * -1 when unsupported (k must be a positive multiple of 256).
+ * smx_q4_0_repack: w (GGUF Q4_0, n rows; gated: 2n rows) -> wp, 16-byte
+ * aligned, smx_q4_0_packed_bytes(n, k, gated) bytes.
+ */
+int64_t smx_q4_0_packed_bytes(int64_t n, int64_t k, int gated);
+int smx_q4_0_repack(void* stream, const void* w, void* wp, int64_t n, int64_t k, int gated);
+
+/*
+ * smx_q4_0_gemm, smx_q4_0_gemm_swiglu, smx_q4_0_gemm_gelu and
+ * smx_q4_0_gemm_argmax over packed weights (smx_q4_0_repack of the same
+ * matrix, gated for the SwiGLU/GELU forms): same arguments, results equal up
+ * to fp32 summation order; k % 256 == 0, x and wp 16-byte aligned.  Same
+ * reference stages as the GGUF forms.
+ */
+int smx_q4_0_gemm_packed(void* stream, const void* x, const void* wp, void* y, int64_t m,
+                         int64_t n, int64_t k);
+int smx_q4_0_gemm_packed_swiglu(void* stream, const void* x, const void* wp, void* out,
+                                int64_t m, int64_t d, int64_t k);
+int smx_q4_0_gemm_packed_gelu(void* stream, const void* x, const void* wp, const void* lut,
+                              void* out, int64_t m, int64_t d, int64_t k);
+int smx_q4_0_gemm_packed_argmax(void* stream, const void* x, const void* wp, void* y,
+                                uint64_t* keys, int64_t m, int64_t n, int64_t k);
 
 /*
  * Paged KV write (vLLM reshape_and_cache): for each token t with

@@ -8,6 +8,14 @@ tests/test_oracle_q4_0.py checks them against each other and against
 known-answer blocks (d = 1.0, -0.0, a subnormal, 65504, +-inf, NaN; the
 nibble order byte 0x1F -> element 0 = 7, element 16 = -7).
 
+repack() restates the packed layout of the batched MFMA GEMM
+(smx_q4_0_repack): the reference repacks its own weights for its kernel at
+load time (src/spark_vllm_ascend/integration/weights.py:42-54); this is the
+MFMA layout's counterpart, pinned by literal known-answer bytes in
+tests/test_oracle_q4_0.py and, on the GPU, by the packed GEMM matching the
+layout-independent float64 GEMV and selecting exact weights for one-hot
+activations.
+
 The third-party routine the reference calls, gguf-py ``dequantize``
 (gguf==0.19.0, deployment/requirements.txt:5), is not installed here; for
 Q4_0 its published algorithm is exactly this closed form: d * (nibble - 8).
@@ -145,3 +153,43 @@ def gemv_np_f64(x_f32: np.ndarray, blocks: np.ndarray, n: int, k: int) -> np.nda
     """numpy restatement of gemv_f64 (independent of the C code)."""
     w = dequant_f32(blocks, n, k).astype(np.float64)
     return w @ np.asarray(x_f32, dtype=np.float64).reshape(k)
+
+
+def packed_groups(n: int, gated: bool) -> int:
+    return -(-n // 8) if gated else -(-n // 16)
+
+
+def packed_bytes(n: int, k: int, gated: bool = False) -> int:
+    return packed_groups(n, gated) * (k // 256) * 2304
+
+
+def repack(blocks: np.ndarray, n: int, k: int, gated: bool = False) -> np.ndarray:
+    """The packed layout of smx_q4_0_repack, uint8 [packed_bytes(n, k, gated)].
+
+    Per row group G (16 rows; gated: gate rows 8G..8G+7 then the matching up
+    rows d + 8G..) and 256-k chunk c, 2304 bytes at (G * k/256 + c) * 2304:
+    lane l = 16 g + r (row r of the group, k-group g) owns 16 bytes at
+    16 l (blocks 0-3 of the chunk) and 1024 + 16 l (blocks 4-7); in them
+    byte 4 i + b holds the codes of elements 8 g + b (low nibble) and
+    8 g + 4 + b (high nibble) of block i; row r's 8 fp16 scales follow at
+    2048 + 16 r.  Rows past the end repeat the last row.  blocks holds n
+    rows (gated: 2n, gate then up)."""
+    assert k % 256 == 0 and k > 0
+    nb, nc = k // BLOCK, k // 256
+    rows_total = 2 * n if gated else n
+    b = np.ascontiguousarray(blocks, dtype=np.uint8).reshape(rows_total, nb, BLOCK_BYTES)
+    qs = b[:, :, 2:]
+    codes = np.concatenate((qs & 15, qs >> 4), axis=-1)       # [rows, nb, 32] element order
+    G = packed_groups(n, gated)
+    r = np.arange(16)
+    if gated:
+        row = np.minimum(8 * np.arange(G)[:, None] + (r & 7)[None, :], n - 1) + n * (r >= 8)[None, :]
+    else:
+        row = np.minimum(16 * np.arange(G)[:, None] + r[None, :], n - 1)
+    cg = codes[row].reshape(G, 16, nc, 8, 4, 8)                # [G, r, c, blk, g, e8]
+    byte = cg[..., :4] | (cg[..., 4:] << 4)                    # [G, r, c, blk, g, b]
+    byte = byte.reshape(G, 16, nc, 2, 4, 4, 4)                 # blk -> (part, i)
+    lanes = byte.transpose(0, 2, 3, 5, 1, 4, 6)                # [G, c, part, g, r, i, b]
+    sc = b[row][:, :, :, :2].reshape(G, 16, nc, 8, 2).transpose(0, 2, 1, 3, 4)  # [G, c, r, blk, 2]
+    out = np.concatenate((lanes.reshape(G, nc, 2048), sc.reshape(G, nc, 256)), axis=-1)
+    return np.ascontiguousarray(out).reshape(-1)

@@ -36,7 +36,8 @@ Kernel sequence (HIP launches):
           RMSNorm(next norm): 7 launches.
   2 <= T <= 16 (one decode token per sequence, over the per-sequence split
           plan SplitKVDecodeBackend.plan built for this step, with the
-          positions and slots): QKV GEMM -> fused planned split-KV + merge
+          positions and slots; the GEMMs read a layer's packed weights when
+          its linears were packed, Q4_0LinearMethod.pack): QKV GEMM -> fused planned split-KV + merge
           -> o_proj GEMM -> add + RMSNorm -> gate|up GEMM with SwiGLU -> down
           GEMM -> add + RMSNorm(next norm).
 Other calls -- no published metadata, more than 16 rows, or rows that are
@@ -58,6 +59,7 @@ import torch
 
 from ..native import torch_ops
 from .attention import SplitKVDecodeMetadata, split_partials
+from .linear import gemm_weight
 
 _layers: dict = {}
 _metadata: SplitKVDecodeMetadata | None = None
@@ -208,16 +210,16 @@ def layer_run(x: torch.Tensor, residual: torch.Tensor, positions: torch.Tensor,
         if md.num_items <= 0:
             raise ValueError("several sequences need this step's split plan "
                              "(SplitKVDecodeBackend.plan with positions and slots)")
-        ops.q4_0_gemm(x, L.qkv.qweight, c.qkv_rows, c.hidden, out=ws["qkv"])
+        ops.q4_0_gemm(x, gemm_weight(L.qkv), c.qkv_rows, c.hidden, out=ws["qkv"])
         ops.qknorm_rope_splitkv_decode_planned_merged(
             ws["qkv"], L.q_norm, L.k_norm, e.cos_sin, kc, vc, md.block_tables, md.plan,
             md.num_items, e.scale, c.eps, c.n_q, ws["po"], ws["pl"], out=ws["attn"])
-        ops.q4_0_gemm(ws["attn"].view(T, -1), L.o_proj.qweight, c.hidden, c.n_q * c.head_dim,
-                      out=ws["o"])
+        ops.q4_0_gemm(ws["attn"].view(T, -1), gemm_weight(L.o_proj), c.hidden,
+                      c.n_q * c.head_dim, out=ws["o"])
         ops.add_rmsnorm(ws["o"], residual, L.post_norm, c.eps, out=ws["h2"],
                         residual_out=ws["res_a"])
-        ops.q4_0_gemm_swiglu(ws["h2"], L.gate_up.qweight, c.intermediate, c.hidden,
-                             out=ws["act"], lut=e.act_lut)
-        ops.q4_0_gemm(ws["act"], L.down.qweight, c.hidden, c.intermediate, out=ws["d"])
+        ops.q4_0_gemm_swiglu(ws["h2"], gemm_weight(L.gate_up, gated=True), c.intermediate,
+                             c.hidden, out=ws["act"], lut=e.act_lut)
+        ops.q4_0_gemm(ws["act"], gemm_weight(L.down), c.hidden, c.intermediate, out=ws["d"])
     ops.add_rmsnorm(ws["d"], ws["res_a"], e.next_norm, c.eps, out=y, residual_out=r_out)
     return y, r_out

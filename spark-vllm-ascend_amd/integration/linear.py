@@ -11,11 +11,18 @@ same hook for Q4_0 linears on vLLM's LinearMethodBase contract:
       registers ``layer.qweight``: uint8 [sum(output_partition_sizes),
       input_size_per_partition/32*18], GGUF Q4_0 blocks as stored in the file.
   process_weights_after_loading(layer)
-      validates the loaded blocks; the kernels stream GGUF blocks directly,
-      so no repack happens.
+      validates the loaded blocks; the GEMVs stream GGUF blocks directly,
+      so no repack happens here.
+  pack(layer, gated=False)
+      on request, for batched decode: adds ``layer.q4_0_packed``, the packed
+      layout of the MFMA GEMM (torch_ops.q4_0_repack; gated for a merged
+      gate|up layer's SwiGLU GEMM), as the reference repacks its weights for
+      its own kernel (src/spark_vllm_ascend/integration/weights.py:42-54).
+      The GGUF blocks stay: the one-row GEMV reads them.
   apply(layer, x, bias=None) -> [..., N] bf16
       one HIP launch: the Q4_0 GEMV for one activation row, the MFMA Q4_0
-      GEMM for 2..16 rows (K % 64 == 0); more rows (prefill) go through the
+      GEMM for 2..16 rows (K % 64 == 0; over the packed weights when pack()
+      made them); more rows (prefill) go through the
       bf16 weights the reference's stock path uses (dequantised on the
       device, then a library GEMM), as Q6HeadMethod defers to the stock
       method outside its one-row case.  Bias added after.
@@ -91,6 +98,21 @@ class Q4_0LinearMethod(_Base):
         if not w.is_contiguous():
             layer.qweight = torch.nn.Parameter(w.contiguous(), requires_grad=False)
 
+    def pack(self, layer: torch.nn.Module, gated: bool = False) -> bool:
+        """Build ``layer.q4_0_packed`` for the batched GEMM (K % 256 == 0;
+        gated: a merged [gate, up] layer of equal halves).  Returns whether
+        the layer has one afterwards."""
+        n, k = layer.q4_0_n, layer.q4_0_k
+        if k % 256 != 0:
+            return False
+        if gated:
+            sizes = layer.output_partition_sizes
+            if len(sizes) != 2 or sizes[0] != sizes[1]:
+                raise ValueError("a gated pack needs a merged [gate, up] layer of equal halves")
+            n = sizes[0]
+        layer.q4_0_packed = torch_ops.q4_0_repack(layer.qweight.reshape(-1), n, k, gated)
+        return True
+
     def apply(self, layer: torch.nn.Module, x: torch.Tensor,
               bias: torch.Tensor | None = None) -> torch.Tensor:
         n, k = layer.q4_0_n, layer.q4_0_k
@@ -108,7 +130,7 @@ class Q4_0LinearMethod(_Base):
         elif m <= GEMM_MAX_ROWS and k % 64 == 0:
             if rows.data_ptr() % 16:
                 rows = rows.clone()  # the tile kernel stages 16-byte activation chunks
-            out = torch_ops.q4_0_gemm(rows, w, n, k)
+            out = torch_ops.q4_0_gemm(rows, gemm_weight(layer), n, k)
         elif m <= GEMM_MAX_ROWS:
             # K % 64 != 0: the GEMV (any K % 32 == 0), one launch per row
             out = torch.empty((m, n), dtype=torch.bfloat16, device=x.device)
@@ -131,6 +153,15 @@ class Q4_0LinearMethod(_Base):
             raise ValueError("apply_swiglu needs a merged [gate, up] layer of equal halves")
         return torch_ops.q4_0_gemv_swiglu(x.reshape(-1), layer.qweight.reshape(-1), sizes[0],
                                           layer.q4_0_k, out=out)
+
+
+def gemm_weight(layer: torch.nn.Module, gated: bool = False):
+    """The weights a batched GEMM of the layer reads: its packed form when
+    pack() made one of that kind, else the GGUF blocks."""
+    p = getattr(layer, "q4_0_packed", None)
+    if p is not None and p.gated == gated:
+        return p
+    return layer.qweight.reshape(-1)
 
 
 class Q4_0Linear(torch.nn.Module):

@@ -42,7 +42,7 @@ import torch
 from ..native import torch_ops
 from .attention import choose_num_splits, choose_plan
 from .head import TiedQ4_0Head
-from .linear import Q4_0Linear
+from .linear import Q4_0Linear, gemm_weight
 from .weights import synthetic_q4_0
 
 
@@ -112,14 +112,16 @@ class DecodeState:
 class DecodeModel:
     """A Q4_0 decoder with random-init weights of a given shape, decoding
     `batch` sequences per step (one token each).  batch == 1 runs the fused
-    GEMV path; batch > 1 runs the MFMA Q4_0 GEMM (m = batch rows) with
-    separate add+RMSNorm launches and the fused q/k-norm + RoPE + KV-write
+    GEMV path; batch > 1 runs the MFMA Q4_0 GEMM (m = batch rows; over the
+    packed weight layout unless packed=False) with separate add+RMSNorm
+    launches and the fused q/k-norm + RoPE + KV-write
     split-KV kernel over a per-sequence split plan (one plan launch per
     step), over a block table with one row per sequence."""
 
     def __init__(self, cfg: DecoderConfig, device, seed: int = 0, max_len: int = 8192,
                  num_splits: int | None = None, weights: dict | None = None,
-                 fused: bool = True, batch: int = 1, plan_items: int | None = None):
+                 fused: bool = True, batch: int = 1, plan_items: int | None = None,
+                 packed: bool = True):
         if not 1 <= batch <= 16:
             raise ValueError("batch must be in [1, 16]")
         if cfg.activation not in ("swiglu", "gelu"):
@@ -165,6 +167,18 @@ class DecodeModel:
         head_blocks = (weights["head"] if weights is not None and "head" in weights
                        else synthetic_q4_0(c.vocab, c.hidden, seed * 1000 + 999, self.device))
         self.head = TiedQ4_0Head(head_blocks.to(self.device), c.vocab, c.hidden)
+        # batch > 1: the MFMA GEMMs read the packed layout (torch_ops.q4_0_repack;
+        # layers whose K is not a multiple of 256 keep the GGUF GEMM); the
+        # one-row GEMVs and the embedding keep reading the GGUF blocks
+        self.head_packed = None
+        if batch > 1 and packed:
+            for L in self.layers:
+                for lin in (L.qkv, L.o_proj, L.down):
+                    lin.quant_method.pack(lin)
+                L.gate_up.quant_method.pack(L.gate_up, gated=True)
+            if c.hidden % 256 == 0:
+                self.head_packed = torch_ops.q4_0_repack(self.head.q4_0_head.view(-1), c.vocab,
+                                                         c.hidden)
         self.cos_sin = rope_cos_sin_cache(max_len, c.head_dim, c.rope_theta, self.device)
         # the GELU table the gate/up epilogues read (None: SwiGLU)
         self.act_lut = torch_ops.gelu_table(self.device) if c.activation == "gelu" else None
@@ -267,18 +281,18 @@ class DecodeModel:
         elif self.batch > 1:
             B = self.batch
             ops.add_rmsnorm(x_in, r_in, L.input_norm, c.eps, out=self.h, residual_out=self.res_a)
-            ops.q4_0_gemm(self.h, L.qkv.qweight, c.qkv_rows, c.hidden, out=self.qkv_out)
+            ops.q4_0_gemm(self.h, gemm_weight(L.qkv), c.qkv_rows, c.hidden, out=self.qkv_out)
             ops.qknorm_rope_splitkv_decode_planned_merged(
                 self.qkv_out, L.q_norm, L.k_norm, self.cos_sin, L.kv_cache[0], L.kv_cache[1],
                 st.block_table, self.plan, self.num_items, self.scale, c.eps, c.n_q,
                 self.partial_o, self.partial_lse, out=self.attn)
-            ops.q4_0_gemm(self.attn.view(B, -1), L.o_proj.qweight, c.hidden, c.n_q * c.head_dim,
-                          out=self.o)
+            ops.q4_0_gemm(self.attn.view(B, -1), gemm_weight(L.o_proj), c.hidden,
+                          c.n_q * c.head_dim, out=self.o)
             ops.add_rmsnorm(self.o, self.res_a, L.post_norm, c.eps, out=self.h2,
                             residual_out=self.res_b)
-            ops.q4_0_gemm_swiglu(self.h2, L.gate_up.qweight, c.intermediate, c.hidden,
-                                 out=self.act, lut=self.act_lut)
-            ops.q4_0_gemm(self.act, L.down.qweight, c.hidden, c.intermediate, out=self.d)
+            ops.q4_0_gemm_swiglu(self.h2, gemm_weight(L.gate_up, gated=True), c.intermediate,
+                                 c.hidden, out=self.act, lut=self.act_lut)
+            ops.q4_0_gemm(self.act, gemm_weight(L.down), c.hidden, c.intermediate, out=self.d)
             return
         else:
             ops.add_rmsnorm(x_in, r_in, L.input_norm, c.eps, out=self.h, residual_out=self.res_a)
@@ -326,8 +340,9 @@ class DecodeModel:
             # nothing (a recorded step must not, see record_runner)
             ops.add_rmsnorm(x_in, r_in, self.final_norm, c.eps, out=self.h,
                             residual_out=self.res_a)
-            ops.q4_0_gemm_argmax(self.h, self.head.q4_0_head, c.vocab, c.hidden,
-                                 self.argmax_keys, out=self.logits)
+            head = self.head_packed if self.head_packed is not None else self.head.q4_0_head
+            ops.q4_0_gemm_argmax(self.h, head, c.vocab, c.hidden, self.argmax_keys,
+                                 out=self.logits)
             keys = self.argmax_keys
         else:
             ops.add_rmsnorm(x_in, r_in, self.final_norm, c.eps, out=self.h,

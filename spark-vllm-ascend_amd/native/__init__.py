@@ -29,7 +29,7 @@ DEFAULT_RECORD = LIB_PATH.with_name("libsmx.validation.json")
 #: benchmark and the build check do (they are what validates and measures the
 #: library as built); a record named by SMX_VALIDATION_RECORD is still checked
 UNVALIDATED_ENV = "SMX_ALLOW_UNVALIDATED"
-ABI_VERSION = 9
+ABI_VERSION = 10
 SMX_EINVAL = 10001
 SMX_EUNSUPPORTED = 10002
 
@@ -67,6 +67,12 @@ SIGNATURES = {
     "smx_q4_0_gemm_gelu": [_P, _P, _P, _P, _P, _I64, _I64, _I64],
     "smx_q4_0_gemm_argmax": [_P, _P, _P, _P, _P, _I64, _I64, _I64],
     "smx_q4_0_gemm_keys_per_row": [_I64],
+    "smx_q4_0_packed_bytes": [_I64, _I64, _I32],
+    "smx_q4_0_repack": [_P, _P, _P, _I64, _I64, _I32],
+    "smx_q4_0_gemm_packed": [_P, _P, _P, _P, _I64, _I64, _I64],
+    "smx_q4_0_gemm_packed_swiglu": [_P, _P, _P, _P, _I64, _I64, _I64],
+    "smx_q4_0_gemm_packed_gelu": [_P, _P, _P, _P, _P, _I64, _I64, _I64],
+    "smx_q4_0_gemm_packed_argmax": [_P, _P, _P, _P, _P, _I64, _I64, _I64],
     "smx_compute_slot_mapping": [_P, _P, _I32, _P, _P, _P, _I32, _I32, _I32, _I32],
     "smx_add_rmsnorm": [_P, _P, _P, _P, _P, _P, _I64, _I64, _F32],
     "smx_qknorm_rope_kv_write": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32,
@@ -102,6 +108,7 @@ RUNNER_FENCES_ACQUIRE_ONLY = 1
 # return types other than int
 RESTYPES = {"smx_q4_0_argmax_keys_size": ctypes.c_int64,
             "smx_q4_0_gemm_keys_per_row": ctypes.c_int64,
+            "smx_q4_0_packed_bytes": ctypes.c_int64,
             "smx_runner_destroy": None}
 
 _lib = None

@@ -377,6 +377,206 @@ hipError_t launch_gemm_tile(hipStream_t s, const void* x, const void* w, void* y
 #undef SMX_GEMM_LAUNCH
   return hipGetLastError();
 }
+
+// ---------------------------------------------------------------------------
+// Packed layout (smx_q4_0_repack): the tile kernel's MFMA B operands stored
+// lane by lane, so a wave reads a 16-row x 256-k chunk with three 16-byte
+// loads and no cross-lane transposes.  Chunk c of row group G is 2304 bytes
+// at (G * nchunks + c) * 2304:
+//   [0, 1024)     lane l (row n = l & 15, k-group g = l >> 4): 16 bytes, word
+//                 i = block i of the chunk, whose byte b holds the codes of the
+//                 block's elements 8 g + b (low nibble) and 8 g + 4 + b (high)
+//   [1024, 2048)  the same for blocks 4..7
+//   [2048, 2304)  row n's 8 fp16 scales at 2048 + 16 n
+// Row n of group G is weight row 16 G + n (plain), or, gated, gate row
+// 8 G + n for n < 8 and up row d + 8 G + n - 8 otherwise; rows past the end
+// repeat the last row (their outputs are never stored).  The bytes are the
+// GGUF blocks' own codes and scales, moved: the repack is lossless.
+// ---------------------------------------------------------------------------
+constexpr int kChunkBytes = 2304;
+
+// One thread per (group, chunk, lane); row-major reads of the GGUF blocks.
+__global__ __launch_bounds__(256) void q4_0_repack_kernel(const uint8_t* __restrict__ w,
+                                                          uint8_t* __restrict__ out, int n_out,
+                                                          int nblocks, int gated, int ngroups) {
+  const int64_t tid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int nchunks = nblocks / 8;
+  if (tid >= (int64_t)ngroups * nchunks * 64) return;
+  const int l = (int)(tid & 63);
+  const int64_t gc = tid >> 6;
+  const int c = (int)(gc % nchunks), G = (int)(gc / nchunks);
+  const int n = l & 15, g = l >> 4;
+  int64_t row;
+  if (gated) row = min(G * 8 + (n & 7), n_out - 1) + (n >= 8 ? (int64_t)n_out : 0);
+  else row = min(G * 16 + n, n_out - 1);
+  const uint8_t* rw = w + row * (int64_t)nblocks * 18;
+  uint8_t* base = out + gc * kChunkBytes;
+#pragma unroll
+  for (int part = 0; part < 2; ++part) {
+    uint32_t words[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint8_t* qs = rw + (c * 8 + part * 4 + i) * 18 + 2;
+      // element e of a block: low nibble of qs[e] (e < 16), else high nibble of qs[e - 16]
+      auto code = [&](int e) -> uint32_t { return e < 16 ? (qs[e] & 15u) : (qs[e - 16] >> 4); };
+      uint32_t wd = 0;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) wd |= (code(8 * g + b) | (code(8 * g + 4 + b) << 4)) << (8 * b);
+      words[i] = wd;
+    }
+    st_agent(reinterpret_cast<u32x4*>(base + part * 1024 + 16 * l),
+             u32x4{words[0], words[1], words[2], words[3]});
+  }
+  if (g == 0) {
+    uint32_t sc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint8_t* b0 = rw + (c * 8 + 2 * i) * 18;
+      const uint8_t* b1 = b0 + 18;
+      sc[i] = (uint32_t)b0[0] | ((uint32_t)b0[1] << 8) | ((uint32_t)b1[0] << 16) | ((uint32_t)b1[1] << 24);
+    }
+    st_agent(reinterpret_cast<u32x4*>(base + 2048 + 16 * n), u32x4{sc[0], sc[1], sc[2], sc[3]});
+  }
+  stores_done();
+}
+
+// The tile kernel's arithmetic over the packed layout: per 256-k chunk a lane
+// loads its 8 blocks' B words and its row's 8 scales directly; the
+// activations are staged through the wave's LDS slice as in the tile kernel
+// (WS 16-byte loads per lane, m <= 2 WS rows).  Per block: MFMA(A, 128 +
+// code), MFMA(A, -136) and the fp32 scale; the waves of a workgroup take the
+// chunks t = wave, wave + ks, ... and are summed in wave order.
+template <bool SWIGLU, int WS, bool KEYS = false>
+__global__ __launch_bounds__(1024) void q4_0_gemm_packed_kernel(
+    const uint8_t* wp, const uint16_t* x_, int nchunks, int n_out, int ks, int m, int64_t ldx,
+    uint16_t* y, int64_t ldy, uint64_t* keys, const uint16_t* act_lut) {
+  static_assert(!(SWIGLU && KEYS), "argmax keys are for plain outputs");
+  __shared__ f32x4 red[16][64];
+  extern __shared__ u32x4 xsl[];  // [ks][2 WS rows x 32 chunks]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n = lane & 15, j = lane >> 4;
+  const uint8_t* gbase = wp + (int64_t)blockIdx.x * nchunks * kChunkBytes;
+  bf16x8 bneg;
+  {
+    const uint32_t c[4] = {kNeg136, kNeg136, kNeg136, kNeg136};
+    bneg = __builtin_bit_cast(bf16x8, c);
+  }
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+  f32x4 acc = zero;
+  const int xrow = min(n, m - 1);  // rows >= m only feed unused C rows
+  for (int t = wave; t < nchunks; t += ks) {
+    const uint8_t* cb = gbase + (int64_t)t * kChunkBytes;
+    const u32x4 wa = *reinterpret_cast<const u32x4*>(cb + 16 * lane);
+    const u32x4 wb = *reinterpret_cast<const u32x4*>(cb + 1024 + 16 * lane);
+    const u32x4 sc = *reinterpret_cast<const u32x4*>(cb + 2048 + 16 * n);
+    u32x4 xa[8];
+    {
+      u32x4* sl = xsl + wave * (WS * 64);
+      u32x4 sv[WS];
+#pragma unroll
+      for (int i = 0; i < WS; ++i) {  // piece q: row q >> 5, 16 bytes (q & 31) of the chunk
+        const int q = i * 64 + lane;
+        sv[i] = *reinterpret_cast<const u32x4*>(x_ + (int64_t)min(q >> 5, m - 1) * ldx + t * 256 +
+                                                (q & 31) * 8);
+      }
+#pragma unroll
+      for (int i = 0; i < WS; ++i) {
+        const int q = i * 64 + lane, r = q >> 5;
+        sl[r * 32 + ((q & 31) ^ (r & 7))] = sv[i];
+      }
+      // the slice is private to this wave (see the tile kernel)
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int b = 0; b < 8; ++b) xa[b] = sl[xrow * 32 + ((4 * b + j) ^ (xrow & 7))];
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    const uint32_t wd[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+    const uint32_t sd[4] = {sc.x, sc.y, sc.z, sc.w};
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      const bf16x8 A = __builtin_bit_cast(bf16x8, xa[b]);
+      f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, dequant_word(wd[b]), zero, 0, 0, 0);
+      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, bneg, c, 0, 0, 0);
+      const float d = f16_bits_to_f32((b & 1) ? (sd[b >> 1] >> 16) : (sd[b >> 1] & 0xffffu));
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[r] = fmaf(d, c[r], acc[r]);
+    }
+  }
+  // C layout: lane l holds rows 4 (l >> 4) + r of column l & 15.
+  red[wave][lane] = acc;
+  __syncthreads();
+  for (int e = threadIdx.x; e < 256; e += 64 * ks) {  // 16 rows x 16 columns
+    const int mr = e >> 4, nn = e & 15;
+    auto total = [&](int col) {
+      float s = 0.f;
+      for (int w = 0; w < ks; ++w) s += red[w][16 * (mr >> 2) + col][mr & 3];
+      return s;
+    };
+    if (mr < m) {
+      if constexpr (SWIGLU) {
+        const int f = blockIdx.x * 8 + nn;
+        if (nn < 8 && f < n_out) {
+          st_agent(y + (int64_t)mr * ldy + f, gated_act(total(nn), total(nn + 8), act_lut));
+        }
+      } else {
+        const int o = blockIdx.x * 16 + nn;
+        if (o < n_out) st_agent(y + (int64_t)mr * ldy + o, f32_to_bf16(total(nn)));
+      }
+    }
+    if constexpr (KEYS && !SWIGLU) {
+      const int o = blockIdx.x * 16 + nn;
+      uint64_t key = 0;
+      if (mr < m && o < n_out)
+        key = ((uint64_t)bf16_order_key(f32_to_bf16(total(nn))) << 32) |
+              (uint64_t)(0xffffffffu - (uint32_t)o);
+#pragma unroll
+      for (int s = 1; s < 16; s <<= 1) {
+        const uint64_t other =
+            ((uint64_t)(uint32_t)__shfl_xor((int)(key >> 32), s, 64) << 32) |
+            (uint32_t)__shfl_xor((int)(uint32_t)key, s, 64);
+        key = other > key ? other : key;
+      }
+      if (nn == 0 && mr < m) st_agent(keys + (int64_t)mr * ((n_out + 15) / 16) + blockIdx.x, key);
+    }
+  }
+  stores_done();
+}
+
+inline int64_t packed_groups(int64_t n, bool gated) { return gated ? (n + 7) / 8 : (n + 15) / 16; }
+
+template <bool SWIGLU, bool KEYS = false>
+hipError_t launch_gemm_packed(hipStream_t s, const void* x, const void* wp, void* y, int64_t m,
+                              int64_t n_out, int64_t k, uint64_t* keys = nullptr,
+                              const uint16_t* act_lut = nullptr) {
+  const int nchunks = (int)(k / 256);
+  const int grid = (int)packed_groups(n_out, SWIGLU);
+  // Waves per workgroup, measured at 8 rows (µs, ks): gate/up 19456x2560
+  // 10.09 (2), 10.28 (3), 11.58 (4); head 151936x2560 60.2 (2), 61.6 (4);
+  // QKV 6144x2560 5.20 (5), 6.17 (10); o_proj 2560x4096 4.58 (10), 6.03 (5);
+  // down 2560x9728 7.41 (10), 9.94 (5).
+  int ks = grid >= 1024 ? 2 : grid >= 256 ? 5 : 10;
+  if (const char* e = tuning_env("SMX_PACKED_KS")) {  // tuning sweeps
+    const int v = atoi(e);
+    if (v >= 1 && v <= 16) ks = v;
+  }
+  ks = ks < nchunks ? ks : nchunks;
+  const int ws = m <= 2 ? 1 : m <= 4 ? 2 : m <= 8 ? 4 : 8;
+  const size_t lds = (size_t)ks * ws * 64 * 16;
+#define SMX_PACKED_LAUNCH(W)                                                                    \
+  SMX_LAUNCH((q4_0_gemm_packed_kernel<SWIGLU, W, KEYS>), dim3(grid), dim3(64 * ks), lds, s,     \
+             (const uint8_t*)wp, (const uint16_t*)x, nchunks, (int)n_out, ks, (int)m, k,         \
+             (uint16_t*)y, n_out, keys, act_lut)
+  if (ws == 1) SMX_PACKED_LAUNCH(1);
+  else if (ws == 2) SMX_PACKED_LAUNCH(2);
+  else if (ws == 4) SMX_PACKED_LAUNCH(4);
+  else SMX_PACKED_LAUNCH(8);
+#undef SMX_PACKED_LAUNCH
+  return hipGetLastError();
+}
 }  // namespace
 }  // namespace smx
 
@@ -437,4 +637,63 @@ extern "C" int smx_q4_0_gemm_argmax(void* stream, const void* x, const void* w, 
   SMX_REQUIRE(keys && (uintptr_t)keys % 8 == 0, "keys must be non-null and 8-byte aligned");
   SMX_REQUIRE((uintptr_t)x % 16 == 0, "x must be 16-byte aligned");
   return (int)smx::launch_gemm_tile<false, true>((hipStream_t)stream, x, w, y, m, n, k, 0, keys);
+}
+
+// ---------------------------------------------------------------------------
+// The packed layout's entry points.
+
+extern "C" int64_t smx_q4_0_packed_bytes(int64_t n, int64_t k, int gated) {
+  if (n < 1 || n > (1ll << 30) || k < 256 || k % 256 != 0 || k > (1 << 20)) return -1;
+  return smx::packed_groups(n, gated != 0) * (k / 256) * smx::kChunkBytes;
+}
+
+extern "C" int smx_q4_0_repack(void* stream, const void* w, void* wp, int64_t n, int64_t k,
+                               int gated) {
+  SMX_REQUIRE(w && wp, "null pointer argument");
+  SMX_REQUIRE(smx_q4_0_packed_bytes(n, k, gated) > 0,
+              "n must be in [1, 2^30] and k a positive multiple of 256 (at most 2^20)");
+  SMX_REQUIRE((uintptr_t)wp % 16 == 0, "wp must be 16-byte aligned");
+  const int64_t groups = smx::packed_groups(n, gated != 0);
+  const int64_t threads = groups * (k / 256) * 64;
+  SMX_LAUNCH(smx::q4_0_repack_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+             (hipStream_t)stream, (const uint8_t*)w, (uint8_t*)wp, (int)n, (int)(k / 32),
+             gated ? 1 : 0, (int)groups);
+  return (int)hipGetLastError();
+}
+
+#define SMX_PACKED_CHECKS(N)                                                                    \
+  SMX_REQUIRE(x && wp && y, "null pointer argument");                                           \
+  SMX_REQUIRE(m >= 1 && m <= 16, "m must be in [1, 16]");                                       \
+  SMX_REQUIRE((N) >= 1 && (N) <= (1ll << 30), "bad output size");                               \
+  SMX_REQUIRE(k >= 256 && k % 256 == 0 && k <= (1 << 20),                                       \
+              "k must be a positive multiple of 256");                                          \
+  SMX_REQUIRE((uintptr_t)x % 16 == 0 && (uintptr_t)wp % 16 == 0 && (uintptr_t)y % 2 == 0,       \
+              "x and wp must be 16-byte aligned")
+
+extern "C" int smx_q4_0_gemm_packed(void* stream, const void* x, const void* wp, void* y,
+                                    int64_t m, int64_t n, int64_t k) {
+  SMX_PACKED_CHECKS(n);
+  return (int)smx::launch_gemm_packed<false>((hipStream_t)stream, x, wp, y, m, n, k);
+}
+
+extern "C" int smx_q4_0_gemm_packed_swiglu(void* stream, const void* x, const void* wp, void* y,
+                                           int64_t m, int64_t d, int64_t k) {
+  SMX_PACKED_CHECKS(d);
+  return (int)smx::launch_gemm_packed<true>((hipStream_t)stream, x, wp, y, m, d, k);
+}
+
+extern "C" int smx_q4_0_gemm_packed_gelu(void* stream, const void* x, const void* wp,
+                                         const void* lut, void* y, int64_t m, int64_t d,
+                                         int64_t k) {
+  SMX_PACKED_CHECKS(d);
+  SMX_REQUIRE(lut && (uintptr_t)lut % 2 == 0, "lut must be non-null and 2-byte aligned");
+  return (int)smx::launch_gemm_packed<true>((hipStream_t)stream, x, wp, y, m, d, k, nullptr,
+                                            (const uint16_t*)lut);
+}
+
+extern "C" int smx_q4_0_gemm_packed_argmax(void* stream, const void* x, const void* wp, void* y,
+                                           uint64_t* keys, int64_t m, int64_t n, int64_t k) {
+  SMX_PACKED_CHECKS(n);
+  SMX_REQUIRE(keys && (uintptr_t)keys % 8 == 0, "keys must be non-null and 8-byte aligned");
+  return (int)smx::launch_gemm_packed<false, true>((hipStream_t)stream, x, wp, y, m, n, k, keys);
 }

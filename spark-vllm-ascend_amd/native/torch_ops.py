@@ -601,32 +601,94 @@ def compute_slot_mapping(query_start_loc: torch.Tensor, positions: torch.Tensor,
     return out
 
 
-def q4_0_gemm(x: torch.Tensor, w: torch.Tensor, n: int, k: int,
-              out: torch.Tensor | None = None) -> torch.Tensor:
-    """y [m, n] = x [m, k] . W^T for m <= 16 rows (MFMA kernel)."""
+class PackedQ4_0:
+    """A Q4_0 matrix in the packed layout of the MFMA GEMMs (smx_q4_0_repack):
+    ``data`` uint8 [packed_bytes], the [n, k] matrix it holds (gated: the
+    [2n, k] gate|up matrix, n = d).  q4_0_gemm, q4_0_gemm_swiglu and
+    q4_0_gemm_argmax take one in place of the GGUF tensor."""
+
+    __slots__ = ("data", "n", "k", "gated")
+
+    def __init__(self, data: torch.Tensor, n: int, k: int, gated: bool):
+        self.data, self.n, self.k, self.gated = data, int(n), int(k), bool(gated)
+
+
+def q4_0_packed_bytes(n: int, k: int, gated: bool = False) -> int:
+    """Bytes of the packed form of an [n, k] Q4_0 matrix (gated: [2n, k]);
+    -1 when unsupported (k not a positive multiple of 256)."""
+    from . import load
+    return int(load().smx_q4_0_packed_bytes(n, k, 1 if gated else 0))
+
+
+def q4_0_repack(w: torch.Tensor, n: int, k: int, gated: bool = False,
+                out: torch.Tensor | None = None) -> PackedQ4_0:
+    """Repack GGUF Q4_0 weights (n rows; gated: the 2n gate|up rows) into the
+    packed layout; lossless (the same codes and fp16 scales, moved)."""
+    nbytes = q4_0_packed_bytes(n, k, gated)
+    _need(nbytes > 0, "the packed layout needs k a positive multiple of 256")
+    _check(w, "w", torch.uint8, (2 * n if gated else n) * q4_0_row_bytes(k))
+    if out is None:
+        out = torch.empty(nbytes, dtype=torch.uint8, device=w.device)
+    _check(out, "out", torch.uint8, nbytes, w.device)
+    _need(out.data_ptr() % 16 == 0, "out must be 16-byte aligned")
+    call("smx_q4_0_repack", _stream(w), w.data_ptr(), out.data_ptr(), n, k, 1 if gated else 0)
+    return PackedQ4_0(out, n, k, gated)
+
+
+def _gemm_x(x: torch.Tensor, k: int, align: int) -> None:
     _need(x.dim() == 2 and x.shape[1] == k and 1 <= x.shape[0] <= 16, "x must be [m <= 16, k]")
     _check(x, "x", BF16)
-    _need(x.data_ptr() % 8 == 0, "x must be 8-byte aligned")
-    _check(w, "w", torch.uint8, n * q4_0_row_bytes(k), x.device)
+    _need(x.data_ptr() % align == 0, f"x must be {align}-byte aligned")
+
+
+def _packed_checked(w: PackedQ4_0, n: int, k: int, gated: bool, device) -> int:
+    _need(w.n == n and w.k == k and w.gated == gated,
+          f"packed weights hold [{w.n}, {w.k}] (gated={w.gated}), the call wants [{n}, {k}] "
+          f"(gated={gated})")
+    _check(w.data, "w.data", torch.uint8, q4_0_packed_bytes(n, k, gated), device)
+    return w.data.data_ptr()
+
+
+def q4_0_gemm(x: torch.Tensor, w: torch.Tensor | PackedQ4_0, n: int, k: int,
+              out: torch.Tensor | None = None) -> torch.Tensor:
+    """y [m, n] = x [m, k] . W^T for m <= 16 rows (MFMA kernel); W GGUF Q4_0
+    or packed (q4_0_repack)."""
+    packed = isinstance(w, PackedQ4_0)
+    _gemm_x(x, k, 16 if packed else 8)
     if out is None:
         out = torch.empty((x.shape[0], n), dtype=BF16, device=x.device)
     _check(out, "out", BF16, x.shape[0] * n, x.device)
-    call("smx_q4_0_gemm", _stream(x), x.data_ptr(), w.data_ptr(), out.data_ptr(), x.shape[0], n, k)
+    if packed:
+        call("smx_q4_0_gemm_packed", _stream(x), x.data_ptr(),
+             _packed_checked(w, n, k, False, x.device), out.data_ptr(), x.shape[0], n, k)
+    else:
+        _check(w, "w", torch.uint8, n * q4_0_row_bytes(k), x.device)
+        call("smx_q4_0_gemm", _stream(x), x.data_ptr(), w.data_ptr(), out.data_ptr(),
+             x.shape[0], n, k)
     return out
 
 
-def q4_0_gemm_swiglu(x: torch.Tensor, w: torch.Tensor, d: int, k: int,
+def q4_0_gemm_swiglu(x: torch.Tensor, w: torch.Tensor | PackedQ4_0, d: int, k: int,
                      out: torch.Tensor | None = None,
                      lut: torch.Tensor | None = None) -> torch.Tensor:
-    """out [m, d] = silu(x W_gate^T) * (x W_up^T), W = [gate; up] [2d, k];
-    given the GELU table (gelu_table) as lut, the table GELU in place of SiLU."""
-    _need(x.dim() == 2 and x.shape[1] == k and 1 <= x.shape[0] <= 16, "x must be [m <= 16, k]")
-    _check(x, "x", BF16)
-    _need(x.data_ptr() % 8 == 0, "x must be 8-byte aligned")
-    _check(w, "w", torch.uint8, 2 * d * q4_0_row_bytes(k), x.device)
+    """out [m, d] = silu(x W_gate^T) * (x W_up^T), W = [gate; up] [2d, k] (GGUF
+    Q4_0, or packed gated by q4_0_repack); given the GELU table (gelu_table)
+    as lut, the table GELU in place of SiLU."""
+    packed = isinstance(w, PackedQ4_0)
+    _gemm_x(x, k, 16 if packed else 8)
     if out is None:
         out = torch.empty((x.shape[0], d), dtype=BF16, device=x.device)
     _check(out, "out", BF16, x.shape[0] * d, x.device)
+    if packed:
+        wp = _packed_checked(w, d, k, True, x.device)
+        if lut is None:
+            call("smx_q4_0_gemm_packed_swiglu", _stream(x), x.data_ptr(), wp, out.data_ptr(),
+                 x.shape[0], d, k)
+        else:
+            call("smx_q4_0_gemm_packed_gelu", _stream(x), x.data_ptr(), wp,
+                 _lut_checked(lut, x.device), out.data_ptr(), x.shape[0], d, k)
+        return out
+    _check(w, "w", torch.uint8, 2 * d * q4_0_row_bytes(k), x.device)
     if lut is None:
         call("smx_q4_0_gemm_swiglu", _stream(x), x.data_ptr(), w.data_ptr(), out.data_ptr(),
              x.shape[0], d, k)
@@ -636,7 +698,7 @@ def q4_0_gemm_swiglu(x: torch.Tensor, w: torch.Tensor, d: int, k: int,
     return out
 
 
-def q4_0_gemm_gelu(x: torch.Tensor, w: torch.Tensor, lut: torch.Tensor, d: int, k: int,
+def q4_0_gemm_gelu(x: torch.Tensor, w: torch.Tensor | PackedQ4_0, lut: torch.Tensor, d: int, k: int,
                    out: torch.Tensor | None = None) -> torch.Tensor:
     return q4_0_gemm_swiglu(x, w, d, k, out, lut)
 
@@ -647,19 +709,22 @@ def gemm_keys_per_row(n: int) -> int:
     return int(load().smx_q4_0_gemm_keys_per_row(n))
 
 
-def q4_0_gemm_argmax(x: torch.Tensor, w: torch.Tensor, n: int, k: int, keys: torch.Tensor,
-                     out: torch.Tensor | None = None) -> torch.Tensor:
-    """y = x W^T (m <= 16 rows) plus keys [m, ceil(n / 16)] int64 (uint64
-    bits), the greedy-argmax keys decode_advance(argmax_keys=keys) reduces."""
-    _need(x.dim() == 2 and x.shape[1] == k and 1 <= x.shape[0] <= 16, "x must be [m <= 16, k]")
+def q4_0_gemm_argmax(x: torch.Tensor, w: torch.Tensor | PackedQ4_0, n: int, k: int,
+                     keys: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """y = x W^T (m <= 16 rows; W GGUF Q4_0 or packed) plus keys [m, ceil(n / 16)]
+    int64 (uint64 bits), the greedy-argmax keys decode_advance(argmax_keys=keys)
+    reduces."""
+    _gemm_x(x, k, 16)
     m = x.shape[0]
-    _check(x, "x", BF16)
-    _need(x.data_ptr() % 16 == 0, "x must be 16-byte aligned")
-    _check(w, "w", torch.uint8, n * q4_0_row_bytes(k), x.device)
     _check(keys, "keys", torch.int64, m * gemm_keys_per_row(n), x.device)
     if out is None:
         out = torch.empty((m, n), dtype=BF16, device=x.device)
     _check(out, "out", BF16, m * n, x.device)
-    call("smx_q4_0_gemm_argmax", _stream(x), x.data_ptr(), w.data_ptr(), out.data_ptr(),
-         keys.data_ptr(), m, n, k)
+    if isinstance(w, PackedQ4_0):
+        call("smx_q4_0_gemm_packed_argmax", _stream(x), x.data_ptr(),
+             _packed_checked(w, n, k, False, x.device), out.data_ptr(), keys.data_ptr(), m, n, k)
+    else:
+        _check(w, "w", torch.uint8, n * q4_0_row_bytes(k), x.device)
+        call("smx_q4_0_gemm_argmax", _stream(x), x.data_ptr(), w.data_ptr(), out.data_ptr(),
+             keys.data_ptr(), m, n, k)
     return out

@@ -5,8 +5,8 @@ src/spark_vllm_ascend/integration/model.py:13-16) through the C ABI:
     the oracle bit for bit (NaN outputs compared as NaN), and a ragged
     shape writes nothing past its output;
   * the fused epilogues -- smx_q4_0_gemv_gelu (streaming and generic
-    kernels), smx_q4_0_add_rmsnorm_gemv_gelu and smx_q4_0_gemm_gelu (tile
-    and word-load kernels) -- equal the oracle bit for bit on one-hot
+    kernels), smx_q4_0_add_rmsnorm_gemv_gelu, smx_q4_0_gemm_gelu (tile
+    and word-load kernels) and smx_q4_0_gemm_packed_gelu -- equal the oracle bit for bit on one-hot
     activations, whose gate/up sums are exact (one product of at most 23
     significant bits), at magnitudes that reach the g / 2, table and
     g-or--0 regions;
@@ -161,20 +161,24 @@ def test_add_rmsnorm_gemv_gelu_one_hot_exact(ops, dev, lut, lut_bits):
     assert _covers_regions(gates)
 
 
-@pytest.mark.parametrize("aligned16", [True, False])
-def test_gemm_gelu_one_hot_exact(ops, dev, lut, lut_bits, aligned16):
+@pytest.mark.parametrize("layout", ["tile", "word", "packed"])
+def test_gemm_gelu_one_hot_exact(ops, dev, lut, lut_bits, layout):
     """8 rows, row r one-hot at its own column with magnitude MAGNITUDES[r]:
-    the tile kernel (16-byte aligned rows) and the word-load kernel (8-byte)."""
+    the tile kernel (16-byte aligned rows), the word-load kernel (8-byte) and
+    the packed-layout kernel (smx_q4_0_gemm_packed_gelu)."""
     import torch
     m, d, k = 8, 200, 512
     blocks = oq.make_blocks(2 * d, k, seed=7, scale=1.0)
     x = np.stack([_one_hot(k, (61 * r + 3) % k, a) for r, a in enumerate(MAGNITUDES)])
     buf = torch.empty(m * k + 8, dtype=torch.bfloat16, device=dev)
-    off = 0 if aligned16 else 4
+    off = 4 if layout == "word" else 0
     xv = buf[off:off + m * k].view(m, k)
-    assert (xv.data_ptr() % 16 == 0) == aligned16
+    assert (xv.data_ptr() % 16 == 0) == (layout != "word")
     xv.copy_(bf16_dev(x, dev))
-    out = bits_of(ops.q4_0_gemm_gelu(xv, _w(blocks, dev), lut, d, k)).reshape(m, d)
+    w = _w(blocks, dev)
+    if layout == "packed":
+        w = ops.q4_0_repack(w, d, k, gated=True)
+    out = bits_of(ops.q4_0_gemm_gelu(xv, w, lut, d, k)).reshape(m, d)
     for r in range(m):
         np.testing.assert_array_equal(_canon(out[r]),
                                       _canon(_exact_gated(x[r], blocks, d, k, lut_bits)),

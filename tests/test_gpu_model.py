@@ -296,6 +296,45 @@ def test_batched_decode_against_per_sequence_oracle(dev, batch, activation):
     assert ties <= max(3, batch * T // 25)
 
 
+@pytest.mark.parametrize("activation", ["swiglu", "gelu"])
+def test_batched_packed_and_gguf_layouts_agree(dev, activation):
+    """A batched model packs every layer linear (gate|up gated) and the head
+    and runs the packed-layout GEMMs; packed=False runs the GGUF-layout GEMMs
+    over the same weights.  The logits of the two agree at every
+    teacher-forced step to within the bf16 rounding of differently ordered
+    fp32 sums, and the greedy tokens match except at near-ties."""
+    import torch
+    m = _m()
+    cfg = tiny_cfg()
+    cfg.activation = activation
+    B, T = 5, 10
+    a = m.DecodeModel(cfg, dev, seed=9, max_len=64, num_splits=3, batch=B)
+    b = m.DecodeModel(cfg, dev, seed=9, max_len=64, num_splits=3, batch=B, packed=False)
+    for L in a.layers:
+        for lin in (L.qkv, L.o_proj, L.down):
+            assert not lin.q4_0_packed.gated
+        assert L.gate_up.q4_0_packed.gated
+    assert a.head_packed is not None and b.head_packed is None
+    assert not hasattr(b.layers[0].qkv, "q4_0_packed")
+    seqs = np.random.default_rng(9).integers(0, cfg.vocab, (B, T))
+    prompts = [torch.from_numpy(s) for s in seqs]
+    a.reset(prompts)
+    b.reset(prompts)
+    diff = 0
+    for pos in range(T):
+        a.step()
+        b.step()
+        torch.cuda.synchronize()
+        la, lb = f32_of(a.logits).reshape(B, -1), f32_of(b.logits).reshape(B, -1)
+        for r in range(B):
+            assert_close_rel(la[r], lb[r], rtol=2e-2, atol_frac=2e-2, what=f"row {r} step {pos}")
+        ia, ib = a.state.next_ids.cpu().numpy(), b.state.next_ids.cpu().numpy()
+        for r in np.nonzero(ia != ib)[0]:
+            assert omodel.top2_margin(lb[r].astype(np.float64))[1] < omodel.NEAR_TIE_REL
+            diff += 1
+    assert diff <= 2
+
+
 def test_batched_graph_replay_and_ragged_prompts(dev):
     """Prompts of different lengths in one batch; graph replay equals eager;
     each row's prompt is fed before its own generated tokens."""

@@ -180,3 +180,87 @@ def test_gemv_bf16_weight_variant_close_to_exact():
     ref = bf16_bits_to_f32(oq.gemv_bf16w_bits(x, blocks, n, k))
     assert np.max(np.abs(ref - exact) / (np.abs(exact) + 0.05)) < 2e-2
     assert np.array_equal(round_bf16(np.float32([1.5])), np.float32([1.5]))
+
+
+def _kat_blocks(rows: int) -> np.ndarray:
+    """rows x 256 weights (8 blocks each), every byte distinct enough to place:
+    scale bytes (0x10 + row, 0x40 + block), qs[j] = (row * 8 + block) * 16 + j
+    (mod 256)."""
+    blk = np.zeros((rows, 8, 18), dtype=np.uint8)
+    for r in range(rows):
+        for j in range(8):
+            blk[r, j, 0], blk[r, j, 1] = 0x10 + r, 0x40 + j
+            blk[r, j, 2:] = ((r * 8 + j) * 16 + np.arange(16)) % 256
+    return blk.reshape(rows, -1)
+
+
+def test_repack_known_bytes():
+    """Literal bytes of the packed layout for a 2-row, 256-k matrix (one group,
+    one chunk).  Row 1 block 7 has qs = 0xF0..0xFF: lane 16*2 + 1 (row 1,
+    k-group 2), byte 1 of word 3 of the second half holds elements 17 and 21
+    = high nibbles of qs[1] = 0xF1 and qs[5] = 0xF5 -> 0xFF; row 0 block 0
+    (qs = 0x00..0x0F), lane 0 byte 0: elements 0 and 4 = low nibbles of qs[0]
+    and qs[4] -> 0x40; lane 16*1 (k-group 1) byte 2: elements 10 and 14 ->
+    0xEA.  Rows 2..15 of the group repeat row 1."""
+    wp = oq.repack(_kat_blocks(2), 2, 256)
+    assert wp.size == 2304 == oq.packed_bytes(2, 256)
+    assert wp[1024 + 16 * (16 * 2 + 1) + 4 * 3 + 1] == 0xFF
+    assert wp[0] == 0x40
+    assert wp[16 * 16 + 2] == 0xEA
+    # row 0, block 1 (qs 0x10..0x1F), k-group 3, byte 3: elements 27 and 31 =
+    # high nibbles of qs[11] = 0x1B and qs[15] = 0x1F -> 0x11
+    assert wp[16 * (16 * 3 + 0) + 4 * 1 + 3] == 0x11
+    # padding row 9 repeats row 1 (block 7 byte as above)
+    assert wp[1024 + 16 * (16 * 2 + 9) + 4 * 3 + 1] == 0xFF
+    # scales: row 1, block 5 -> bytes (0x11, 0x45) at 2048 + 16 + 10
+    assert (wp[2048 + 16 + 10], wp[2048 + 16 + 11]) == (0x11, 0x45)
+    assert (wp[2048 + 16 * 15 + 14], wp[2048 + 16 * 15 + 15]) == (0x11, 0x47)
+
+
+def test_repack_known_bytes_gated():
+    """Gated, d = 3 (rows 0-2 gate, 3-5 up): lane row r < 8 is gate row
+    min(r, 2), r >= 8 up row 3 + min(r - 8, 2).  Row 5 block 0 has qs = 0x80 +
+    j: lane row 10, k-group 0, byte 0 -> elements 0, 4 = 0x0, 0x4 -> 0x40;
+    its scale bytes are (0x15, 0x40)."""
+    wp = oq.repack(_kat_blocks(6), 3, 256, gated=True)
+    assert wp.size == 2304 == oq.packed_bytes(3, 256, gated=True)
+    assert (wp[2048 + 16 * 10], wp[2048 + 16 * 10 + 1]) == (0x15, 0x40)
+    assert (wp[2048 + 16 * 8], wp[2048 + 16 * 8 + 1]) == (0x13, 0x40)
+    assert (wp[2048 + 16 * 5], wp[2048 + 16 * 5 + 1]) == (0x12, 0x40)
+    assert (wp[2048 + 16 * 1], wp[2048 + 16 * 1 + 1]) == (0x11, 0x40)
+    assert wp[16 * 10] == 0x40
+    # row 3 (up 0) block 2: qs = (3*8+2)*16 + j = 0xA0 + j; lane row 8,
+    # k-group 1, byte 0: elements 8, 12 = low nibbles of 0xA8, 0xAC -> 0xC8
+    assert wp[16 * (16 * 1 + 8) + 4 * 2 + 0] == 0xC8
+
+
+@pytest.mark.parametrize("n,k,gated", [(40, 512, False), (37, 768, True), (16, 256, False)])
+def test_repack_is_lossless(n, k, gated):
+    """Every code and scale of every row reappears at its place: decoding the
+    packed bytes back (loops over the layout's definition) gives the
+    dequantised matrix, and the packed size is the GGUF size rounded up to
+    whole row groups."""
+    rows = 2 * n if gated else n
+    blocks = oq.make_blocks(rows, k, seed=n + k)
+    wp = oq.repack(blocks, n, k, gated)
+    G, nc = oq.packed_groups(n, gated), k // 256
+    assert wp.size == G * nc * 2304
+    w = oq.dequant_f32(blocks, rows, k)
+    got = np.full((rows, k), np.nan, dtype=np.float32)
+    for Gi in range(G):
+        for c in range(nc):
+            ch = wp[(Gi * nc + c) * 2304:(Gi * nc + c + 1) * 2304]
+            for r in range(16):
+                if gated:
+                    row = (n + min(8 * Gi + r - 8, n - 1)) if r >= 8 else min(8 * Gi + r, n - 1)
+                else:
+                    row = min(16 * Gi + r, n - 1)
+                scales = ch[2048 + 16 * r:2048 + 16 * r + 16].copy().view("<f2").astype(np.float32)
+                for g in range(4):
+                    for blk in range(8):
+                        off = (blk // 4) * 1024 + 16 * (16 * g + r) + 4 * (blk % 4)
+                        for b in range(4):
+                            byte = int(ch[off + b])
+                            for e, code in ((8 * g + b, byte & 15), (8 * g + 4 + b, byte >> 4)):
+                                got[row, c * 256 + blk * 32 + e] = scales[blk] * (code - 8)
+    np.testing.assert_array_equal(got, w)
