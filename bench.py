@@ -420,8 +420,10 @@ def batch_breakdown(model, ctx, reps: int = 10):
     36 gate/up launches.  Resets the contexts first, and leaves the model's
     state advanced."""
     from spark_vllm_ascend_amd.native import torch_ops as ops
+    from spark_vllm_ascend_amd.integration.linear import gemm_weight as gw
     m, c, st, L = model, model.cfg, model.state, model.layers
     n, B = len(L), model.batch
+    head_w = m.head_packed if m.head_packed is not None else m.head.q4_0_head
     m.set_context(list(ctx))
     ops.splitkv_plan(st.seq_lens, st.block_table, c.block_size, m.num_items, m.partial_o,
                      m.partial_lse, positions=st.positions, slot_mapping=st.slot_mapping,
@@ -429,21 +431,21 @@ def batch_breakdown(model, ctx, reps: int = 10):
     kernels = {
         "norm_in": ("residual add + input RMSNorm, B rows", 1, lambda i: ops.add_rmsnorm(
             m.d, m.res_b, L[i].input_norm, c.eps, out=m.h, residual_out=m.res_a)),
-        "qkv": ("QKV GEMM 6144x2560, m = B", 1, lambda i: ops.q4_0_gemm(
-            m.h, L[i].qkv.qweight, c.qkv_rows, c.hidden, out=m.qkv_out)),
+        "qkv": ("QKV GEMM 6144x2560 (packed weights), m = B", 1, lambda i: ops.q4_0_gemm(
+            m.h, gw(L[i].qkv), c.qkv_rows, c.hidden, out=m.qkv_out)),
         "attention": ("q/k norm + RoPE + KV write + split-KV over the plan, then the LSE merge "
                       "(two launches)", 2, lambda i: ops.qknorm_rope_splitkv_decode_planned_merged(
             m.qkv_out, L[i].q_norm, L[i].k_norm, m.cos_sin, L[i].kv_cache[0], L[i].kv_cache[1],
             st.block_table, m.plan, m.num_items, m.scale, c.eps, c.n_q, m.partial_o,
             m.partial_lse, out=m.attn)),
-        "o_proj": ("o_proj GEMM 2560x4096, m = B", 1, lambda i: ops.q4_0_gemm(
-            m.attn.view(B, -1), L[i].o_proj.qweight, c.hidden, c.n_q * c.head_dim, out=m.o)),
+        "o_proj": ("o_proj GEMM 2560x4096 (packed weights), m = B", 1, lambda i: ops.q4_0_gemm(
+            m.attn.view(B, -1), gw(L[i].o_proj), c.hidden, c.n_q * c.head_dim, out=m.o)),
         "norm_post": ("residual add + post-attention RMSNorm, B rows", 1, lambda i: ops.add_rmsnorm(
             m.o, m.res_a, L[i].post_norm, c.eps, out=m.h2, residual_out=m.res_b)),
-        "gate_up": ("gate/up GEMM 19456x2560 + SwiGLU, m = B", 1, lambda i: ops.q4_0_gemm_swiglu(
-            m.h2, L[i].gate_up.qweight, c.intermediate, c.hidden, out=m.act)),
-        "down": ("down GEMM 2560x9728, m = B", 1, lambda i: ops.q4_0_gemm(
-            m.act, L[i].down.qweight, c.hidden, c.intermediate, out=m.d)),
+        "gate_up": ("gate/up GEMM 19456x2560 + SwiGLU (packed weights), m = B", 1, lambda i: ops.q4_0_gemm_swiglu(
+            m.h2, gw(L[i].gate_up, gated=True), c.intermediate, c.hidden, out=m.act)),
+        "down": ("down GEMM 2560x9728 (packed weights), m = B", 1, lambda i: ops.q4_0_gemm(
+            m.act, gw(L[i].down), c.hidden, c.intermediate, out=m.d)),
     }
     out = {}
     for key, (what, launches, f) in kernels.items():
@@ -453,8 +455,7 @@ def batch_breakdown(model, ctx, reps: int = 10):
 
     def head():
         ops.add_rmsnorm(m.d, m.res_b, m.final_norm, c.eps, out=m.h)
-        ops.q4_0_gemm_argmax(m.h, m.head.q4_0_head, c.vocab, c.hidden, m.argmax_keys,
-                             out=m.logits)
+        ops.q4_0_gemm_argmax(m.h, head_w, c.vocab, c.hidden, m.argmax_keys, out=m.logits)
 
     def advance():
         ops.decode_advance(st.next_ids, st.ids, st.positions, st.seq_lens, st.slot_mapping,
@@ -463,7 +464,7 @@ def batch_breakdown(model, ctx, reps: int = 10):
                            argmax_keys=m.argmax_keys, embed_table=m.head.weight, embed_out=m.x)
     base = time_graph(lambda: [gu(i) for i in range(n)], n, reps) * n
     with_head = time_graph(lambda: ([gu(i) for i in range(n)], head()), n + 2, reps) * (n + 2)
-    out["head"] = {"what": "final add+RMSNorm + Q4_0 head GEMM 151936x2560 + argmax keys",
+    out["head"] = {"what": "final add+RMSNorm + Q4_0 head GEMM 151936x2560 (packed weights) + argmax keys",
                    "us_per_step": round(with_head - base, 3)}
     m.set_context(list(ctx))
     with_adv = time_graph(lambda: ([gu(i) for i in range(n)], advance()), n + 1, reps) * (n + 1)
