@@ -444,14 +444,14 @@ __global__ __launch_bounds__(256) void q4_0_repack_kernel(const uint8_t* __restr
 // loads its 8 blocks' B words and its row's 8 scales directly; the
 // activations are staged through the wave's LDS slice as in the tile kernel
 // (WS 16-byte loads per lane, m <= 2 WS rows).  Per block: MFMA(A, 128 +
-// code), MFMA(A, -136) and the fp32 scale; the waves of a workgroup take the
-// chunks t = wave, wave + ks, ... and are summed in wave order.
+// code), MFMA(A, -136) and the fp32 scale; the waves of a workgroup (ks <=
+// 10) take the chunks t = wave, wave + ks, ... and are summed in wave order.
 template <bool SWIGLU, int WS, bool KEYS = false>
-__global__ __launch_bounds__(1024) void q4_0_gemm_packed_kernel(
+__global__ __launch_bounds__(640) void q4_0_gemm_packed_kernel(
     const uint8_t* wp, const uint16_t* x_, int nchunks, int n_out, int ks, int m, int64_t ldx,
     uint16_t* y, int64_t ldy, uint64_t* keys, const uint16_t* act_lut) {
   static_assert(!(SWIGLU && KEYS), "argmax keys are for plain outputs");
-  __shared__ f32x4 red[16][64];
+  __shared__ f32x4 red[10][64];
   extern __shared__ u32x4 xsl[];  // [ks][2 WS rows x 32 chunks]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n = lane & 15, j = lane >> 4;
@@ -464,21 +464,27 @@ __global__ __launch_bounds__(1024) void q4_0_gemm_packed_kernel(
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
   f32x4 acc = zero;
   const int xrow = min(n, m - 1);  // rows >= m only feed unused C rows
-  for (int t = wave; t < nchunks; t += ks) {
+  // chunk t + ks's weights and activations are loaded while chunk t is
+  // computed (the next chunk's loads are issued once this chunk's registers
+  // have been consumed)
+  u32x4 wa, wb, sc, sv[WS];
+  auto load = [&](int t) {
     const uint8_t* cb = gbase + (int64_t)t * kChunkBytes;
-    const u32x4 wa = *reinterpret_cast<const u32x4*>(cb + 16 * lane);
-    const u32x4 wb = *reinterpret_cast<const u32x4*>(cb + 1024 + 16 * lane);
-    const u32x4 sc = *reinterpret_cast<const u32x4*>(cb + 2048 + 16 * n);
+    wa = *reinterpret_cast<const u32x4*>(cb + 16 * lane);
+    wb = *reinterpret_cast<const u32x4*>(cb + 1024 + 16 * lane);
+    sc = *reinterpret_cast<const u32x4*>(cb + 2048 + 16 * n);
+#pragma unroll
+    for (int i = 0; i < WS; ++i) {  // piece q: row q >> 5, 16 bytes (q & 31) of the chunk
+      const int q = i * 64 + lane;
+      sv[i] = *reinterpret_cast<const u32x4*>(x_ + (int64_t)min(q >> 5, m - 1) * ldx + t * 256 +
+                                              (q & 31) * 8);
+    }
+  };
+  if (wave < nchunks) load(wave);
+  for (int t = wave; t < nchunks; t += ks) {
     u32x4 xa[8];
     {
       u32x4* sl = xsl + wave * (WS * 64);
-      u32x4 sv[WS];
-#pragma unroll
-      for (int i = 0; i < WS; ++i) {  // piece q: row q >> 5, 16 bytes (q & 31) of the chunk
-        const int q = i * 64 + lane;
-        sv[i] = *reinterpret_cast<const u32x4*>(x_ + (int64_t)min(q >> 5, m - 1) * ldx + t * 256 +
-                                                (q & 31) * 8);
-      }
 #pragma unroll
       for (int i = 0; i < WS; ++i) {
         const int q = i * 64 + lane, r = q >> 5;
@@ -496,6 +502,7 @@ __global__ __launch_bounds__(1024) void q4_0_gemm_packed_kernel(
     }
     const uint32_t wd[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
     const uint32_t sd[4] = {sc.x, sc.y, sc.z, sc.w};
+    if (t + ks < nchunks) load(t + ks);
 #pragma unroll
     for (int b = 0; b < 8; ++b) {
       const bf16x8 A = __builtin_bit_cast(bf16x8, xa[b]);
@@ -555,13 +562,13 @@ hipError_t launch_gemm_packed(hipStream_t s, const void* x, const void* wp, void
   const int nchunks = (int)(k / 256);
   const int grid = (int)packed_groups(n_out, SWIGLU);
   // Waves per workgroup, measured at 8 rows (µs, ks): gate/up 19456x2560
-  // 10.09 (2), 10.28 (3), 11.58 (4); head 151936x2560 60.2 (2), 61.6 (4);
-  // QKV 6144x2560 5.20 (5), 6.17 (10); o_proj 2560x4096 4.58 (10), 6.03 (5);
-  // down 2560x9728 7.41 (10), 9.94 (5).
+  // 9.39 (2), 10.22 (3); head 151936x2560 57.3 (2), 58.1 (3); QKV 6144x2560
+  // 5.25 (6), 5.31 (4), 6.37 (10); o_proj 2560x4096 4.46 (8), 4.50 (10),
+  // 5.25 (4); down 2560x9728 7.41 (10), 7.51 (8), 9.48 (4).
   int ks = grid >= 1024 ? 2 : grid >= 256 ? 5 : 10;
   if (const char* e = tuning_env("SMX_PACKED_KS")) {  // tuning sweeps
     const int v = atoi(e);
-    if (v >= 1 && v <= 16) ks = v;
+    if (v >= 1 && v <= 10) ks = v;
   }
   ks = ks < nchunks ? ks : nchunks;
   const int ws = m <= 2 ? 1 : m <= 4 ? 2 : m <= 8 ? 4 : 8;
