@@ -480,12 +480,13 @@ def batch_breakdown(model, ctx, reps: int = 10):
 
 
 def batch_decode(dev, steps: int = 64, warmup: int = 4, batch: int = 8, seed: int = 5,
-                 breakdown: bool = True):
+                 breakdown: bool = True, executor: str = "runner"):
     """Config-5 style throughput: `batch` sequences at seeded ragged contexts
     ~U[512, 32768] decoded together through the captured step graph (MFMA
     GEMM path, split-KV over per-sequence block tables), over a KV cache
     filled with seeded random bf16; with `breakdown`, the unprofiled
-    per-class times of that step (batch_breakdown)."""
+    per-class times of that step (batch_breakdown).  executor "graph"
+    times the captured graph only (no step runner is recorded)."""
     import torch
     from spark_vllm_ascend_amd.integration.model import DecodeModel, DecoderConfig
     ctx = torch.randint(512, 32768, (batch,), generator=torch.Generator().manual_seed(seed))
@@ -494,7 +495,9 @@ def batch_decode(dev, steps: int = 64, warmup: int = 4, batch: int = 8, seed: in
     model.fill_kv(seed)
     model.set_context(ctx.tolist())
     model.capture()
-    executor, runner_error = record_runner(model)
+    runner_error = None
+    if executor == "runner":
+        executor, runner_error = record_runner(model)
     model.set_context(ctx.tolist())
     _untimed_steps(model, warmup, executor)
     dt = _timed_steps(model, steps, executor) / steps
@@ -732,6 +735,10 @@ def main() -> int:
                     help="no per-kernel step breakdown (e.g. under a profiler)")
     ap.add_argument("--cpu-budget", type=float, default=25.0,
                     help="seconds per decode-step leg of the CPU baseline")
+    ap.add_argument("--executor", choices=["runner", "graph"], default="runner",
+                    help="batch phase: time the step runner (and the graph beside it), or the "
+                         "captured graph alone (rocprofv3's kernel trace does not run the "
+                         "runner's replays of the 8-sequence step)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the decode path has no multi-GPU launch (it would "
@@ -749,7 +756,8 @@ def main() -> int:
         print(json.dumps(counter_workload(dev)))
         return 0
     if args.phase == "batch":
-        print(json.dumps(batch_decode(dev, breakdown=not args.skip_breakdown)))
+        print(json.dumps(batch_decode(dev, breakdown=not args.skip_breakdown,
+                                      executor=args.executor)))
         return 0
 
     if args.phase in ("all", "roofline"):
