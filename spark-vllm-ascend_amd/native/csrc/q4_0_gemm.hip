@@ -662,6 +662,7 @@ extern "C" int smx_q4_0_repack(void* stream, const void* w, void* wp, int64_t n,
   SMX_REQUIRE((uintptr_t)wp % 16 == 0, "wp must be 16-byte aligned");
   const int64_t groups = smx::packed_groups(n, gated != 0);
   const int64_t threads = groups * (k / 256) * 64;
+  SMX_REQUIRE((threads + 255) / 256 <= 0x7fffffff, "matrix too large for one repack launch");
   SMX_LAUNCH(smx::q4_0_repack_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
              (hipStream_t)stream, (const uint8_t*)w, (uint8_t*)wp, (int)n, (int)(k / 32),
              gated ? 1 : 0, (int)groups);

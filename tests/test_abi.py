@@ -155,3 +155,28 @@ def test_graph_num_nodes_rejects_null():
     native = pkg("native")
     n = ctypes.c_int64(-1)
     assert native.load().smx_graph_num_nodes(None, ctypes.byref(n)) == native.SMX_EINVAL
+
+
+def test_packed_layout_sizes_and_host_checks():
+    """smx_q4_0_packed_bytes: whole 16-row groups (gated: 8 gate + 8 up rows) of
+    2304 bytes per 256-k chunk, -1 off the supported shapes; smx_q4_0_repack
+    and the packed GEMMs refuse bad shapes on the host, before any launch
+    (the pointers below are never dereferenced)."""
+    native = pkg("native")
+    lib = native.load()
+    assert lib.smx_q4_0_packed_bytes(16, 256, 0) == 2304
+    assert lib.smx_q4_0_packed_bytes(17, 256, 0) == 2 * 2304
+    assert lib.smx_q4_0_packed_bytes(9728, 2560, 1) == 1216 * 10 * 2304
+    assert lib.smx_q4_0_packed_bytes(2560, 9728, 0) == 2560 * 9728 // 32 * 18
+    for n, k in ((0, 256), (16, 0), (16, 320), (16, 128), (16, 1 << 21), ((1 << 30) + 1, 256)):
+        assert lib.smx_q4_0_packed_bytes(n, k, 0) == -1, (n, k)
+    E = native.SMX_EINVAL
+    assert lib.smx_q4_0_repack(None, 16, 32, 16, 320, 0) == E      # k not a multiple of 256
+    assert lib.smx_q4_0_repack(None, 16, 40, 16, 256, 0) == E      # wp not 16-byte aligned
+    assert lib.smx_q4_0_repack(None, None, 32, 16, 256, 0) == E
+    assert lib.smx_q4_0_repack(None, 16, 32, 1 << 30, 1 << 20, 0) == E  # grid beyond one launch
+    assert lib.smx_q4_0_gemm_packed(None, 32, 32, 32, 17, 16, 256) == E   # m > 16
+    assert lib.smx_q4_0_gemm_packed(None, 40, 32, 32, 2, 16, 256) == E    # x not 16-byte aligned
+    assert lib.smx_q4_0_gemm_packed_swiglu(None, 32, 32, 32, 2, 16, 320) == E
+    assert lib.smx_q4_0_gemm_packed_gelu(None, 32, 32, None, 32, 2, 16, 256) == E  # no table
+    assert lib.smx_q4_0_gemm_packed_argmax(None, 32, 32, 32, None, 2, 16, 256) == E  # no keys
