@@ -86,6 +86,37 @@ def test_apply_dispatch(dev, monkeypatch, m, n, k, launches):
     torch.testing.assert_close(y3.view(m, n), y + bias, rtol=0, atol=0)
 
 
+@pytest.mark.parametrize("m,n,k,launches", [
+    (1, 6144, 2560, ["smx_q4_0_gemv"]),
+    (8, 6144, 2560, ["smx_q4_0_gemm_packed"]),
+    (16, 2560, 4096, ["smx_q4_0_gemm_packed"]),
+    (3, 512, 2592, ["smx_q4_0_gemv"] * 3),        # K % 256 != 0: not packed
+    (4, 512, 320, ["smx_q4_0_gemm"]),             # K % 64 == 0 but not packed: GGUF GEMM
+])
+def test_apply_dispatch_with_packed_weights(dev, monkeypatch, m, n, k, launches):
+    """Q4_0Config(pack_for_batch=True): process_weights_after_loading adds the
+    packed layout where K % 256 == 0, and apply() runs the packed GEMM for
+    2..16 rows, the GEMV for one, against the same float64 oracle."""
+    import torch
+    lin_mod = pkg("integration.linear")
+    layer = lin_mod.Q4_0Linear(k, [n], device=dev)
+    layer.quant_method = lin_mod.Q4_0Config(pack_for_batch=True).get_quant_method(layer)
+    blocks = oq.make_blocks(n, k, seed=m * 37 + n)
+    layer.qweight.data.copy_(torch.from_numpy(blocks))
+    layer.quant_method.process_weights_after_loading(layer)
+    assert hasattr(layer, "q4_0_packed") == (k % 256 == 0)
+    rng = np.random.default_rng(m + k + 1)
+    x_bits = randn_bf16(rng, (m, k))
+    seen = _count_calls(monkeypatch)
+    y = layer(bf16_dev(x_bits, dev))
+    torch.cuda.synchronize()
+    assert seen == launches
+    got = f32_of(y).reshape(m, n)
+    for r in range(m):
+        assert_close_rel(got[r], oq.gemv_f64(x_bits[r], blocks, n, k), rtol=1e-2,
+                         atol_frac=5e-3, what=f"row {r}")
+
+
 def _tiny_cfg():
     m = pkg("integration.model")
     return m.DecoderConfig(hidden=256, n_layers=2, n_q=8, n_kv=2, head_dim=128,
