@@ -447,10 +447,16 @@ def batch_breakdown(model, ctx, reps: int = 10):
         "down": ("down GEMM 2560x9728 (packed weights), m = B", 1, lambda i: ops.q4_0_gemm(
             m.act, gw(L[i].down), c.hidden, c.intermediate, out=m.d)),
     }
+    rb = lambda rows, k: rows * k // 32 * 18
+    weight_bytes = {"qkv": rb(c.qkv_rows, c.hidden), "o_proj": rb(c.hidden, c.n_q * c.head_dim),
+                    "gate_up": rb(2 * c.intermediate, c.hidden),
+                    "down": rb(c.hidden, c.intermediate)}
     out = {}
     for key, (what, launches, f) in kernels.items():
         us = time_graph(lambda: [f(i) for i in range(n)], n * launches, reps) * launches
         out[key] = {"what": what, "us_per_layer": round(us, 3)}
+        if key in weight_bytes:  # the GEMMs: Q4_0 weight bytes streamed per microsecond
+            out[key]["weight_gbs"] = round(weight_bytes[key] / us / 1e3, 1)
     gu = kernels["gate_up"][2]
 
     def head():
