@@ -236,12 +236,16 @@ class DecodeModel:
     @classmethod
     def from_gguf(cls, path, device, max_len: int = 8192, num_splits: int | None = None,
                   block_size: int = 128, fused: bool = True,
-                  activation: str = "swiglu") -> "DecodeModel":
+                  activation: str = "swiglu", batch: int = 1,
+                  packed: bool = True) -> "DecodeModel":
         """A model whose weights come from a local GGUF file (Q4_0 linears and
         head, float norms rounded to bf16), shapes from its metadata.  GGUF
         metadata does not name the gate activation, so it is an argument:
         "swiglu" (the 4B Q4_0 decoder) or "gelu", the reference model's
-        table erf-GELU (src/spark_vllm_ascend/integration/model.py:13-16)."""
+        table erf-GELU (src/spark_vllm_ascend/integration/model.py:13-16).
+        batch / packed: as for the constructor (batch > 1 decodes that many
+        sequences per step, over the packed weight layout unless packed is
+        False)."""
         from .gguf_file import GGUFFile, decoder_config, decoder_weights
         if activation not in ("swiglu", "gelu"):
             raise ValueError(f"activation must be 'swiglu' or 'gelu', got {activation!r}")
@@ -252,7 +256,8 @@ class DecodeModel:
         for k, v in decoder_weights(g, cfg.n_layers).items():
             t = torch.from_numpy(v.copy())
             w[k] = (t.to(torch.bfloat16) if t.dtype == torch.float32 else t).to(dev)
-        return cls(cfg, dev, max_len=max_len, num_splits=num_splits, weights=w, fused=fused)
+        return cls(cfg, dev, max_len=max_len, num_splits=num_splits, weights=w, fused=fused,
+                   batch=batch, packed=packed)
 
     # ------------------------------------------------------------------ step
     def _layer_input(self, i: int):

@@ -203,6 +203,41 @@ def test_model_from_gguf_against_oracle(tmp_path, activation):
                          what=f"logits at {pos}")
 
 
+@pytest.mark.gpu
+def test_batched_model_from_gguf_against_oracle(tmp_path):
+    """The same file decoding two sequences per step (MFMA GEMMs; the 512-k
+    o_proj over the packed layout, the 128-k linears and head over GGUF
+    blocks), each row teacher-forced against its own oracle decoder."""
+    import torch
+    from oracle import model as omodel
+    from oracle.bf16 import round_bf16
+    from _util import assert_close_rel, f32_of
+    p, _ = tiny_qwen3_file(tmp_path)
+    mm = pkg("integration.model")
+    dev = torch.device("cuda:0")
+    model = mm.DecodeModel.from_gguf(p, dev, max_len=64, block_size=32, batch=2)
+    L0 = model.layers[0]
+    assert L0.o_proj.q4_0_packed is not None and not hasattr(L0.qkv, "q4_0_packed")
+    g = gf().GGUFFile(p)
+    cfg = gf().decoder_config(g)
+    w = {k: (round_bf16(v) if v.dtype == np.float32 else v)
+         for k, v in gf().decoder_weights(g, cfg["n_layers"]).items()}
+    ocfg = {k: cfg[k] for k in ("hidden", "n_layers", "n_q", "n_kv", "head_dim", "intermediate",
+                                "vocab", "eps")}
+    cap = model.state.block_table.shape[1] * 32
+    oracles = [omodel.OracleDecoder(ocfg, w, f32_of(model.cos_sin), num_splits=2, capacity=cap)
+               for _ in range(2)]
+    seqs = np.array([[3, 17, 200, 5, 77, 128, 9, 250], [41, 0, 255, 90, 12, 33, 7, 64]])
+    model.reset([torch.from_numpy(s) for s in seqs])
+    for pos in range(seqs.shape[1]):
+        model.step()
+        torch.cuda.synchronize()
+        gl = f32_of(model.logits).reshape(2, -1)
+        for r in range(2):
+            ol = oracles[r].step(int(seqs[r, pos]), pos)
+            assert_close_rel(gl[r], ol, rtol=2e-2, atol_frac=2e-2, what=f"row {r} at {pos}")
+
+
 def test_from_gguf_rejects_an_unknown_activation(tmp_path):
     mm = pkg("integration.model")
     with pytest.raises(ValueError, match="activation"):
